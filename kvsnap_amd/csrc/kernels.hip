@@ -1,0 +1,624 @@
+// gfx950 kernels of the KV snapshot dataplane, behind a plain C ABI.
+//
+//   restore  packed records (pinned host memory, read in place over the host
+//            link, or a device staging buffer) -> each (block, span) written
+//            to span_base + block_id * span_pitch.  Replaces the reference's
+//            Triton restore kernel (kvsnap/connector/copy_kernel.py:22-49).
+//   gather   the inverse: KV cache spans -> block-major packed records.
+//            Replaces save_gather's index_select + cat
+//            (kvsnap/connector/dataplane.py:409-417).
+//   zero     byte ranges of a record set to zero: the token slots past the last
+//            computed token (kvsnap/connector/dataplane.py:262-272).
+//   crc32c   per-record CRC32C (reflected 0x82F63B78, init/xorout ~0), bit
+//            exact with csrc/dataplane/io.cpp:16-47.
+//   sha256   per-record SHA-256 digest, the blob id of
+//            kvsnap/connector/volatile.py:151 and kvsnap/store/store.py:622.
+//   synth    seeded synthetic KV bytes (bench and test input only).
+//
+// A "span" is one contiguous run of a block inside one cache tensor: one per
+// layer for [blocks, H, N, C] caches (the reference's layout), two per layer
+// (K then V) for [2, blocks, N, H, C] caches.  Span s of block b lives at
+// span_base[s] + b * span_pitch[s], is span_words[s] 8-byte words long and
+// sits at byte span_offset[s] of the block's packed record.  All tables are
+// int64 arrays in device memory, as in the reference's launch contract.
+//
+// No MFMA anywhere: nothing on this path is a contraction.  The copies are
+// 16-byte-per-lane streams (one dwordx4 per lane, 8 in flight per lane), the
+// CRC is LDS table lookups combined in GF(2), and SHA-256 is one record per
+// lane because the hash is a sequential chain within a record.
+#include <hip/hip_runtime.h>
+
+#include "common.h"
+
+#include <cstdint>
+#include <cstring>
+#include <mutex>
+#include <stdexcept>
+#include <string>
+
+namespace {
+
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kThreads = 256;   // copy and CRC workgroups: 4 waves
+constexpr int kUnroll = 8;      // dwordx4 loads in flight per lane in the copy loop
+
+// ----------------------------------------------------------------- copies
+
+// Copy nbytes (a multiple of 8; src and dst 8-byte aligned) with the whole
+// workgroup.  The 16-byte path covers everything when both ends are 16-byte
+// aligned, which the host tables normally guarantee.
+__device__ __forceinline__ void copy_span(const char* __restrict__ src, char* __restrict__ dst,
+                                          int64_t nbytes) {
+    const int tid = threadIdx.x;
+    int64_t done = 0;
+    if (((reinterpret_cast<uintptr_t>(src) | reinterpret_cast<uintptr_t>(dst)) & 15) == 0) {
+        const u32x4* s = reinterpret_cast<const u32x4*>(src);
+        u32x4* d = reinterpret_cast<u32x4*>(dst);
+        const int64_t nv = nbytes >> 4;
+        int64_t i = tid;
+        for (; i + (kUnroll - 1) * kThreads < nv; i += kUnroll * kThreads) {
+            u32x4 v[kUnroll];
+#pragma unroll
+            for (int u = 0; u < kUnroll; ++u) v[u] = __builtin_nontemporal_load(s + i + u * kThreads);
+#pragma unroll
+            for (int u = 0; u < kUnroll; ++u) __builtin_nontemporal_store(v[u], d + i + u * kThreads);
+        }
+        for (; i < nv; i += kThreads) __builtin_nontemporal_store(__builtin_nontemporal_load(s + i), d + i);
+        done = nv << 4;
+    }
+    const uint64_t* s8 = reinterpret_cast<const uint64_t*>(src + done);
+    uint64_t* d8 = reinterpret_cast<uint64_t*>(dst + done);
+    const int64_t nw = (nbytes - done) >> 3;
+    for (int64_t i = tid; i < nw; i += kThreads) d8[i] = s8[i];
+}
+
+// Job j = (block j / n_spans, span j % n_spans): the reference kernel's
+// order (copy_kernel.py:29-31), so a launch walks its records front to back.
+__global__ __launch_bounds__(kThreads) void restore_kernel(
+    const int64_t* __restrict__ sources, const int64_t* __restrict__ blocks, int64_t n_blocks,
+    const int64_t* __restrict__ offs, const int64_t* __restrict__ bases, const int64_t* __restrict__ pitches,
+    const int64_t* __restrict__ words, int64_t n_spans) {
+    const int64_t jobs = n_blocks * n_spans;
+    for (int64_t job = blockIdx.x; job < jobs; job += gridDim.x) {
+        const int64_t b = job / n_spans, s = job - b * n_spans;
+        const char* src = reinterpret_cast<const char*>(sources[b] + offs[s]);
+        char* dst = reinterpret_cast<char*>(bases[s] + blocks[b] * pitches[s]);
+        copy_span(src, dst, words[s] * 8);
+    }
+}
+
+__global__ __launch_bounds__(kThreads) void gather_kernel(
+    const int64_t* __restrict__ blocks, int64_t n_blocks, const int64_t* __restrict__ offs,
+    const int64_t* __restrict__ bases, const int64_t* __restrict__ pitches, const int64_t* __restrict__ words,
+    int64_t n_spans, char* __restrict__ records, int64_t record_pitch) {
+    const int64_t jobs = n_blocks * n_spans;
+    for (int64_t job = blockIdx.x; job < jobs; job += gridDim.x) {
+        const int64_t b = job / n_spans, s = job - b * n_spans;
+        const char* src = reinterpret_cast<const char*>(bases[s] + blocks[b] * pitches[s]);
+        char* dst = records + b * record_pitch + offs[s];
+        copy_span(src, dst, words[s] * 8);
+    }
+}
+
+// One workgroup per region; regions are small (one token's C elements).
+__global__ __launch_bounds__(kThreads) void zero_kernel(char* __restrict__ base, const int64_t* __restrict__ offsets,
+                                                       const int64_t* __restrict__ lengths, int64_t n) {
+    for (int64_t r = blockIdx.x; r < n; r += gridDim.x) {
+        char* p = base + offsets[r];
+        const int64_t len = lengths[r];
+        for (int64_t i = threadIdx.x; i < len; i += kThreads) p[i] = 0;
+    }
+}
+
+// ----------------------------------------------------------------- synthetic KV
+// Integer-only generator, bit-identical to the oracle's C version.
+
+__device__ __forceinline__ uint64_t mix64(uint64_t z) {
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    return z ^ (z >> 31);
+}
+
+__device__ __forceinline__ uint64_t span_key(uint64_t seed, uint64_t span, uint64_t block) {
+    uint64_t h = mix64(seed + 0x9E3779B97F4A7C15ull);
+    h = mix64(h + span * 0xD1B54A32D192ED03ull);
+    return mix64(h + block * 0xABC98388FB8FAC03ull);
+}
+
+__device__ __forceinline__ float normal_sample(uint64_t key, uint64_t element) {
+    const uint64_t r = mix64(key + element * 0x9E3779B97F4A7C15ull);
+    const int32_t sum = static_cast<int32_t>(r & 0xFFFF) + static_cast<int32_t>((r >> 16) & 0xFFFF) +
+                        static_cast<int32_t>((r >> 32) & 0xFFFF) + static_cast<int32_t>(r >> 48);
+    return __fmul_rn(static_cast<float>(sum - 131070), 2.6429e-05f);
+}
+
+__device__ __forceinline__ uint32_t to_bf16(float x) {
+    const uint32_t u = __float_as_uint(x);
+    return (u + 0x7FFFu + ((u >> 16) & 1u)) >> 16;
+}
+
+__device__ __forceinline__ uint32_t to_e4m3(float x) {
+    const uint32_t u = __float_as_uint(x);
+    const uint32_t sign = (u >> 24) & 0x80u;
+    const uint32_t a = u & 0x7FFFFFFFu;
+    if (a >= 0x43E00000u) return sign | 0x7Eu;
+    if (a < 0x3C800000u) {
+        const float q = __fmul_rn(__uint_as_float(a), 512.0f);
+        uint32_t n = static_cast<uint32_t>(q);
+        const float frac = __fsub_rn(q, static_cast<float>(n));
+        if (frac > 0.5f || (frac == 0.5f && (n & 1u))) ++n;
+        return sign | n;
+    }
+    const uint32_t rounded = a + 0x7FFFFu + ((a >> 20) & 1u);
+    const uint32_t exp = (rounded >> 23) - 127 + 7;
+    const uint32_t man = (rounded >> 20) & 7u;
+    uint32_t code = (exp << 3) | man;
+    if (code > 0x7Eu) code = 0x7Eu;
+    return sign | code;
+}
+
+__global__ __launch_bounds__(kThreads) void synth_kernel(uint64_t seed, int kind, const int64_t* __restrict__ bases,
+                                                        const int64_t* __restrict__ pitches,
+                                                        const int64_t* __restrict__ words,
+                                                        const float* __restrict__ inv_scales, int64_t n_spans,
+                                                        int64_t first_block, int64_t n_blocks) {
+    const int64_t jobs = n_blocks * n_spans;
+    for (int64_t job = blockIdx.x; job < jobs; job += gridDim.x) {
+        const int64_t b = first_block + job / n_spans, s = job % n_spans;
+        u32x4* dst = reinterpret_cast<u32x4*>(bases[s] + b * pitches[s]);
+        const int64_t nv = words[s] / 2;  // 16-byte vectors
+        const uint64_t key = span_key(seed, static_cast<uint64_t>(s), static_cast<uint64_t>(b));
+        const float inv = inv_scales ? inv_scales[s] : 1.0f;
+        for (int64_t v = threadIdx.x; v < nv; v += kThreads) {
+            uint32_t w[4];
+            if (kind == 0) {
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const uint64_t e = static_cast<uint64_t>(v) * 8 + 2 * i;
+                    w[i] = to_bf16(normal_sample(key, e)) | (to_bf16(normal_sample(key, e + 1)) << 16);
+                }
+            } else if (kind == 1) {
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    uint32_t word = 0;
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) {
+                        const uint64_t e = static_cast<uint64_t>(v) * 16 + 4 * i + j;
+                        word |= to_e4m3(__fmul_rn(normal_sample(key, e), inv)) << (8 * j);
+                    }
+                    w[i] = word;
+                }
+            } else {
+#pragma unroll
+                for (int i = 0; i < 2; ++i) {
+                    const uint64_t r = mix64(key + (static_cast<uint64_t>(v) * 2 + i) * 0x9E3779B97F4A7C15ull);
+                    w[2 * i] = static_cast<uint32_t>(r);
+                    w[2 * i + 1] = static_cast<uint32_t>(r >> 32);
+                }
+            }
+            dst[v] = u32x4{w[0], w[1], w[2], w[3]};
+        }
+    }
+}
+
+// ----------------------------------------------------------------- CRC32C
+//
+// Linear algebra of the reflected CRC (all arithmetic in GF(2)):
+//   the register after a message M of N bytes from start value s0 is
+//     shift(s0, N) ^ R(M),
+//   where shift(s, n) advances s by n zero bytes (multiplication by x^(8n)
+//   mod P) and R is the "raw" CRC from a zero register, which is linear and
+//   satisfies R(A || B) = shift(R(A), |B|) ^ R(B) and R(0^k || A) = R(A).
+// So a record can be cut into equal stripes (the first one padded in front
+// with virtual zero bytes) whose raw CRCs are computed independently and
+// combined by Horner's rule; crc32c = ~(shift(~prior, N) ^ R(record)).
+//
+// Inside a stripe, lane t of a 256-lane workgroup reads the 16-byte word at
+// t*16 of every 4 KiB group (fully coalesced), folds it with
+//   acc = shift(acc, 4096) ^ R16(word),
+// and finally contributes shift(acc, (255 - t) * 16); the workgroup's XOR of
+// those is the stripe's raw CRC.  Tables (in LDS):
+//   T[k][v]  = shift(v, 4 - k)             slicing-by-4 for R16,
+//   G[k][v]  = shift(v << 8k, 4096)        the per-group advance.
+// Per-lane constants M[t] = x^(8 * 16 * (255 - t)) mod P are applied with a
+// bitwise GF(2) multiply.
+
+constexpr uint32_t kPoly = 0x82F63B78u;
+constexpr int kGroup = kThreads * 16;  // bytes per group
+constexpr int kStripeGroups = 16;      // groups per stripe: 64 KiB stripes
+constexpr int kCrcGrid = 2048;         // persistent workgroups
+
+__device__ uint32_t g_crc_tables[256 * 4 + 256 * 4 + 256];
+
+__device__ __forceinline__ uint32_t gf_mul(uint32_t a, uint32_t b) {
+    // a * b mod P in the reflected representation (bit 31 is x^0).
+    uint32_t p = 0;
+#pragma unroll
+    for (int i = 0; i < 32; ++i) {
+        p ^= b & (0u - ((a >> (31 - i)) & 1u));
+        b = (b >> 1) ^ (kPoly & (0u - (b & 1u)));
+    }
+    return p;
+}
+
+__device__ __forceinline__ uint32_t slice4(const uint32_t (*t)[256], uint32_t x) {
+    return t[0][x & 0xFF] ^ t[1][(x >> 8) & 0xFF] ^ t[2][(x >> 16) & 0xFF] ^ t[3][x >> 24];
+}
+
+template <bool kAligned>
+__global__ __launch_bounds__(kThreads) void crc_stripes_kernel(const uint8_t* __restrict__ records, uint64_t pitch,
+                                                              int64_t n_records, int64_t stripes, int64_t groups,
+                                                              uint64_t pad, uint32_t* __restrict__ partial) {
+    __shared__ uint32_t t4[4][256];
+    __shared__ uint32_t tg[4][256];
+    __shared__ uint32_t red[kThreads / 64];
+    for (int i = threadIdx.x; i < 1024; i += kThreads) {
+        t4[i >> 8][i & 255] = g_crc_tables[i];
+        tg[i >> 8][i & 255] = g_crc_tables[1024 + i];
+    }
+    const uint32_t lane_shift = g_crc_tables[2048 + threadIdx.x];
+    __syncthreads();
+    const int64_t jobs = n_records * stripes;
+    const int64_t stripe_bytes = groups * kGroup;
+    for (int64_t job = blockIdx.x; job < jobs; job += gridDim.x) {
+        const int64_t r = job / stripes, j = job - r * stripes;
+        const uint8_t* rec = records + r * pitch;
+        uint32_t acc = 0;
+        for (int64_t g = 0; g < groups; ++g) {
+            const int64_t virt = j * stripe_bytes + g * kGroup + threadIdx.x * 16;
+            const int64_t at = virt - static_cast<int64_t>(pad);
+            uint32_t w0 = 0, w1 = 0, w2 = 0, w3 = 0;
+            if (kAligned) {
+                if (at >= 0) {
+                    const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(rec + at));
+                    w0 = v.x; w1 = v.y; w2 = v.z; w3 = v.w;
+                }
+            } else {
+                uint32_t w[4] = {0, 0, 0, 0};
+                for (int k = 0; k < 16; ++k)
+                    if (at + k >= 0) w[k >> 2] |= static_cast<uint32_t>(rec[at + k]) << (8 * (k & 3));
+                w0 = w[0]; w1 = w[1]; w2 = w[2]; w3 = w[3];
+            }
+            uint32_t s = slice4(t4, w0);
+            s = slice4(t4, s ^ w1);
+            s = slice4(t4, s ^ w2);
+            s = slice4(t4, s ^ w3);
+            acc = slice4(tg, acc) ^ s;
+        }
+        uint32_t v = gf_mul(lane_shift, acc);
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) v ^= __shfl_xor(v, o);
+        if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+        __syncthreads();
+        if (threadIdx.x == 0) partial[job] = red[0] ^ red[1] ^ red[2] ^ red[3];
+        __syncthreads();
+    }
+}
+
+__global__ __launch_bounds__(64) void crc_combine_kernel(const uint32_t* __restrict__ partial, int64_t n_records,
+                                                         int64_t stripes, uint32_t stripe_shift, uint32_t init_term,
+                                                         uint32_t* __restrict__ out) {
+    const int64_t r = static_cast<int64_t>(blockIdx.x) * 64 + threadIdx.x;
+    if (r >= n_records) return;
+    uint32_t s = 0;
+    for (int64_t j = 0; j < stripes; ++j) s = gf_mul(stripe_shift, s) ^ partial[r * stripes + j];
+    out[r] = ~(init_term ^ s);
+}
+
+// ----------------------------------------------------------------- SHA-256 (FIPS 180-4)
+
+__constant__ uint32_t kSha[64] = {
+    0x428a2f98, 0x71374491, 0xb5c0fbcf, 0xe9b5dba5, 0x3956c25b, 0x59f111f1, 0x923f82a4, 0xab1c5ed5,
+    0xd807aa98, 0x12835b01, 0x243185be, 0x550c7dc3, 0x72be5d74, 0x80deb1fe, 0x9bdc06a7, 0xc19bf174,
+    0xe49b69c1, 0xefbe4786, 0x0fc19dc6, 0x240ca1cc, 0x2de92c6f, 0x4a7484aa, 0x5cb0a9dc, 0x76f988da,
+    0x983e5152, 0xa831c66d, 0xb00327c8, 0xbf597fc7, 0xc6e00bf3, 0xd5a79147, 0x06ca6351, 0x14292967,
+    0x27b70a85, 0x2e1b2138, 0x4d2c6dfc, 0x53380d13, 0x650a7354, 0x766a0abb, 0x81c2c92e, 0x92722c85,
+    0xa2bfe8a1, 0xa81a664b, 0xc24b8b70, 0xc76c51a3, 0xd192e819, 0xd6990624, 0xf40e3585, 0x106aa070,
+    0x19a4c116, 0x1e376c08, 0x2748774c, 0x34b0bcb5, 0x391c0cb3, 0x4ed8aa4a, 0x5b9cca4f, 0x682e6ff3,
+    0x748f82ee, 0x78a5636f, 0x84c87814, 0x8cc70208, 0x90befffa, 0xa4506ceb, 0xbef9a3f7, 0xc67178f2,
+};
+
+__device__ __forceinline__ uint32_t rotr(uint32_t x, int n) { return (x >> n) | (x << (32 - n)); }
+
+// w[0..15] are the block's big-endian message words.
+__device__ __forceinline__ void sha_compress(uint32_t h[8], uint32_t w[16]) {
+    uint32_t a = h[0], b = h[1], c = h[2], d = h[3], e = h[4], f = h[5], g = h[6], hh = h[7];
+#pragma unroll
+    for (int t = 0; t < 64; ++t) {
+        uint32_t wt;
+        if (t < 16) {
+            wt = w[t];
+        } else {
+            const uint32_t x15 = w[(t - 15) & 15], x2 = w[(t - 2) & 15];
+            const uint32_t s0 = rotr(x15, 7) ^ rotr(x15, 18) ^ (x15 >> 3);
+            const uint32_t s1 = rotr(x2, 17) ^ rotr(x2, 19) ^ (x2 >> 10);
+            wt = w[t & 15] + s0 + w[(t - 7) & 15] + s1;
+            w[t & 15] = wt;
+        }
+        const uint32_t t1 = hh + (rotr(e, 6) ^ rotr(e, 11) ^ rotr(e, 25)) + ((e & f) | (~e & g)) + kSha[t] + wt;
+        const uint32_t ab = a ^ b;
+        const uint32_t t2 = (rotr(a, 2) ^ rotr(a, 13) ^ rotr(a, 22)) + ((ab & c) | (~ab & b));
+        hh = g; g = f; f = e; e = d + t1; d = c; c = b; b = a; a = t1 + t2;
+    }
+    h[0] += a; h[1] += b; h[2] += c; h[3] += d; h[4] += e; h[5] += f; h[6] += g; h[7] += hh;
+}
+
+__device__ __forceinline__ uint32_t bswap(uint32_t x) { return __builtin_bswap32(x); }
+
+// One record per lane; a wave hashes 64 records side by side.
+template <bool kAligned>
+__global__ __launch_bounds__(64) void sha256_kernel(const uint8_t* __restrict__ records, uint64_t record_bytes,
+                                                    uint64_t pitch, int64_t n_records, uint32_t* __restrict__ out) {
+    const int64_t r = static_cast<int64_t>(blockIdx.x) * 64 + threadIdx.x;
+    if (r >= n_records) return;
+    const uint8_t* p = records + r * pitch;
+    uint32_t h[8] = {0x6a09e667, 0xbb67ae85, 0x3c6ef372, 0xa54ff53a, 0x510e527f, 0x9b05688c, 0x1f83d9ab, 0x5be0cd19};
+    const uint64_t whole = record_bytes / 64;
+    uint32_t w[16];
+    if (kAligned) {
+        const u32x4* q = reinterpret_cast<const u32x4*>(p);
+        u32x4 cur[4];
+        if (whole) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) cur[i] = q[i];
+        }
+        for (uint64_t blk = 0; blk < whole; ++blk) {
+            u32x4 nxt[4];
+            const u32x4* nq = q + 4 * (blk + 1 < whole ? blk + 1 : blk);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) nxt[i] = nq[i];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                w[4 * i] = bswap(cur[i].x);
+                w[4 * i + 1] = bswap(cur[i].y);
+                w[4 * i + 2] = bswap(cur[i].z);
+                w[4 * i + 3] = bswap(cur[i].w);
+            }
+            sha_compress(h, w);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) cur[i] = nxt[i];
+        }
+    } else {
+        for (uint64_t blk = 0; blk < whole; ++blk) {
+            const uint8_t* bp = p + 64 * blk;
+#pragma unroll
+            for (int i = 0; i < 16; ++i)
+                w[i] = static_cast<uint32_t>(bp[4 * i]) << 24 | static_cast<uint32_t>(bp[4 * i + 1]) << 16 |
+                       static_cast<uint32_t>(bp[4 * i + 2]) << 8 | static_cast<uint32_t>(bp[4 * i + 3]);
+            sha_compress(h, w);
+        }
+    }
+    // Final block(s): the rest of the record, 0x80, zeros, 64-bit bit length.
+    const uint64_t rest = record_bytes - 64 * whole;
+    const uint8_t* tail = p + 64 * whole;
+    const int nfinal = rest + 9 <= 64 ? 1 : 2;
+    const uint64_t bits = record_bytes * 8;
+    for (int f = 0; f < nfinal; ++f) {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            uint32_t word = 0;
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const uint64_t pos = static_cast<uint64_t>(64 * f + 4 * i + k);
+                uint32_t byte = 0;
+                if (pos < rest)
+                    byte = tail[pos];
+                else if (pos == rest)
+                    byte = 0x80;
+                else if (pos >= static_cast<uint64_t>(64 * nfinal - 8))
+                    byte = static_cast<uint32_t>(bits >> (8 * (64 * nfinal - 1 - pos))) & 0xFF;
+                word |= byte << (24 - 8 * k);
+            }
+            w[i] = word;
+        }
+        sha_compress(h, w);
+    }
+    u32x4* o = reinterpret_cast<u32x4*>(out + 8 * r);
+    o[0] = u32x4{bswap(h[0]), bswap(h[1]), bswap(h[2]), bswap(h[3])};
+    o[1] = u32x4{bswap(h[4]), bswap(h[5]), bswap(h[6]), bswap(h[7])};
+}
+
+// ----------------------------------------------------------------- host helpers
+
+uint32_t host_gf_mul(uint32_t a, uint32_t b) {
+    uint32_t p = 0;
+    for (int i = 0; i < 32; ++i) {
+        if ((a >> (31 - i)) & 1u) p ^= b;
+        b = (b >> 1) ^ (kPoly & (0u - (b & 1u)));
+    }
+    return p;
+}
+
+// x^(8n) mod P, by squaring from x^(2^k).
+uint32_t host_xpow8n(uint64_t n) {
+    uint32_t sq = 0x40000000u;  // x^1
+    uint32_t result = 0x80000000u;  // x^0
+    uint64_t e = n * 8;
+    while (e) {
+        if (e & 1) result = host_gf_mul(sq, result);
+        sq = host_gf_mul(sq, sq);
+        e >>= 1;
+    }
+    return result;
+}
+
+uint32_t host_shift(uint32_t s, uint64_t nbytes) { return host_gf_mul(host_xpow8n(nbytes), s); }
+
+std::mutex g_table_mutex;
+bool g_tables_ready[64];
+
+void ensure_crc_tables() {
+    int device = 0;
+    if (hipGetDevice(&device) != hipSuccess || device < 0 || device >= 64)
+        throw std::runtime_error("no current HIP device for the CRC32C tables");
+    std::lock_guard<std::mutex> lock(g_table_mutex);
+    if (g_tables_ready[device]) return;
+    static uint32_t tables[256 * 4 + 256 * 4 + 256];
+    const uint32_t group_shift = host_xpow8n(kGroup);
+    for (uint32_t k = 0; k < 4; ++k)
+        for (uint32_t v = 0; v < 256; ++v) {
+            tables[256 * k + v] = host_shift(v, 4 - k);
+            tables[1024 + 256 * k + v] = host_gf_mul(group_shift, v << (8 * k));
+        }
+    for (uint32_t t = 0; t < 256; ++t) tables[2048 + t] = host_xpow8n(16ull * (255 - t));
+    hipError_t rc = hipMemcpyToSymbol(HIP_SYMBOL(g_crc_tables), tables, sizeof tables, 0, hipMemcpyHostToDevice);
+    if (rc != hipSuccess) throw std::runtime_error(std::string("CRC32C table upload: ") + hipGetErrorString(rc));
+    g_tables_ready[device] = true;
+}
+
+template <typename F>
+int guard(F&& f) {
+    try {
+        f();
+        return 0;
+    } catch (const std::exception& e) {
+        kvsnap::set_error(e.what());
+        return -1;
+    }
+}
+
+void check_launch(const char* what) {
+    hipError_t rc = hipGetLastError();
+    if (rc != hipSuccess) throw std::runtime_error(std::string(what) + " launch: " + hipGetErrorString(rc));
+}
+
+unsigned grid_for(int64_t jobs, int programs) {
+    int64_t grid = programs > 0 ? (programs < jobs ? programs : jobs) : jobs;
+    if (grid > (int64_t(1) << 30)) grid = int64_t(1) << 30;
+    return static_cast<unsigned>(grid);
+}
+
+struct CrcPlan {
+    int64_t groups, stripes;
+    uint64_t pad;
+};
+
+CrcPlan crc_plan(uint64_t record_bytes) {
+    CrcPlan plan;
+    plan.groups = record_bytes >= static_cast<uint64_t>(kStripeGroups) * kGroup ? kStripeGroups : 1;
+    const uint64_t stripe_bytes = static_cast<uint64_t>(plan.groups) * kGroup;
+    plan.stripes = static_cast<int64_t>((record_bytes + stripe_bytes - 1) / stripe_bytes);
+    if (plan.stripes == 0) plan.stripes = 1;
+    plan.pad = static_cast<uint64_t>(plan.stripes) * stripe_bytes - record_bytes;
+    return plan;
+}
+
+}  // namespace
+
+extern "C" {
+
+int kvsnap_kernels_abi_version() { return 1; }
+
+int kvsnap_restore_blocks(const int64_t* sources, const int64_t* blocks, int64_t n_blocks,
+                          const int64_t* span_offsets, const int64_t* span_bases, const int64_t* span_pitches,
+                          const int64_t* span_words, int64_t n_spans, int programs, uintptr_t stream) {
+    return guard([&] {
+        if (n_blocks < 0 || n_spans < 0) throw std::runtime_error("negative restore size");
+        if (n_blocks == 0 || n_spans == 0) return;
+        if (!sources || !blocks || !span_offsets || !span_bases || !span_pitches || !span_words)
+            throw std::runtime_error("restore tables must be device pointers");
+        hipLaunchKernelGGL(restore_kernel, dim3(grid_for(n_blocks * n_spans, programs)), dim3(kThreads), 0,
+                           reinterpret_cast<hipStream_t>(stream), sources, blocks, n_blocks, span_offsets,
+                           span_bases, span_pitches, span_words, n_spans);
+        check_launch("restore");
+    });
+}
+
+int kvsnap_gather_blocks(const int64_t* blocks, int64_t n_blocks, const int64_t* span_offsets,
+                         const int64_t* span_bases, const int64_t* span_pitches, const int64_t* span_words,
+                         int64_t n_spans, void* records, int64_t record_pitch, int programs, uintptr_t stream) {
+    return guard([&] {
+        if (n_blocks < 0 || n_spans < 0 || record_pitch < 0) throw std::runtime_error("negative gather size");
+        if (n_blocks == 0 || n_spans == 0) return;
+        if (!records || !blocks || !span_offsets || !span_bases || !span_pitches || !span_words)
+            throw std::runtime_error("gather tables must be device pointers");
+        hipLaunchKernelGGL(gather_kernel, dim3(grid_for(n_blocks * n_spans, programs)), dim3(kThreads), 0,
+                           reinterpret_cast<hipStream_t>(stream), blocks, n_blocks, span_offsets, span_bases,
+                           span_pitches, span_words, n_spans, static_cast<char*>(records), record_pitch);
+        check_launch("gather");
+    });
+}
+
+int kvsnap_zero_regions(void* base, const int64_t* offsets, const int64_t* lengths, int64_t n, uintptr_t stream) {
+    return guard([&] {
+        if (n < 0) throw std::runtime_error("negative region count");
+        if (n == 0) return;
+        if (!base || !offsets || !lengths) throw std::runtime_error("zero regions need device pointers");
+        hipLaunchKernelGGL(zero_kernel, dim3(grid_for(n, 1024)), dim3(kThreads), 0,
+                           reinterpret_cast<hipStream_t>(stream), static_cast<char*>(base), offsets, lengths, n);
+        check_launch("zero");
+    });
+}
+
+int kvsnap_synth_fill(uint64_t seed, int kind, const int64_t* span_bases, const int64_t* span_pitches,
+                      const int64_t* span_words, const float* span_inv_scales, int64_t n_spans, int64_t first_block,
+                      int64_t n_blocks, uintptr_t stream) {
+    return guard([&] {
+        if (kind < 0 || kind > 2) throw std::runtime_error("unknown synthetic kind");
+        if (n_spans < 0 || n_blocks < 0 || first_block < 0) throw std::runtime_error("negative synth size");
+        if (n_spans == 0 || n_blocks == 0) return;
+        hipLaunchKernelGGL(synth_kernel, dim3(grid_for(n_blocks * n_spans, 8192)), dim3(kThreads), 0,
+                           reinterpret_cast<hipStream_t>(stream), seed, kind, span_bases, span_pitches, span_words,
+                           span_inv_scales, n_spans, first_block, n_blocks);
+        check_launch("synth");
+    });
+}
+
+size_t kvsnap_crc32c_workspace_bytes(uint64_t record_bytes, int64_t n_records) {
+    if (n_records <= 0) return 0;
+    return static_cast<size_t>(crc_plan(record_bytes).stripes) * static_cast<size_t>(n_records) * sizeof(uint32_t);
+}
+
+int kvsnap_crc32c_records(const void* records, uint64_t record_bytes, uint64_t record_pitch, int64_t n_records,
+                          uint32_t prior, uint32_t* out, void* workspace, size_t workspace_bytes, uintptr_t stream) {
+    return guard([&] {
+        if (n_records < 0) throw std::runtime_error("negative record count");
+        if (n_records == 0) return;
+        if (!out || (!records && record_bytes)) throw std::runtime_error("CRC32C needs device pointers");
+        const CrcPlan plan = crc_plan(record_bytes);
+        const size_t need = static_cast<size_t>(plan.stripes) * static_cast<size_t>(n_records) * sizeof(uint32_t);
+        if (!workspace || workspace_bytes < need) throw std::runtime_error("CRC32C workspace too small");
+        ensure_crc_tables();
+        hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+        const bool aligned = (reinterpret_cast<uintptr_t>(records) % 16 == 0) && (record_pitch % 16 == 0) &&
+                             (record_bytes % 16 == 0);
+        const unsigned grid = grid_for(n_records * plan.stripes, kCrcGrid);
+        auto* partial = static_cast<uint32_t*>(workspace);
+        const auto* base = static_cast<const uint8_t*>(records);
+        if (aligned)
+            hipLaunchKernelGGL(crc_stripes_kernel<true>, dim3(grid), dim3(kThreads), 0, s, base, record_pitch, n_records, plan.stripes, plan.groups, plan.pad, partial);
+        else
+            hipLaunchKernelGGL(crc_stripes_kernel<false>, dim3(grid), dim3(kThreads), 0, s, base, record_pitch, n_records, plan.stripes, plan.groups, plan.pad, partial);
+        check_launch("crc32c stripes");
+        const uint32_t stripe_shift = host_xpow8n(static_cast<uint64_t>(plan.groups) * kGroup);
+        const uint32_t init_term = host_shift(~prior, record_bytes);
+        hipLaunchKernelGGL(crc_combine_kernel, dim3(static_cast<unsigned>((n_records + 63) / 64)), dim3(64), 0, s,
+                           partial, n_records, plan.stripes, stripe_shift, init_term, out);
+        check_launch("crc32c combine");
+    });
+}
+
+int kvsnap_sha256_records(const void* records, uint64_t record_bytes, uint64_t record_pitch, int64_t n_records,
+                          uint8_t* out, uintptr_t stream) {
+    return guard([&] {
+        if (n_records < 0) throw std::runtime_error("negative record count");
+        if (n_records == 0) return;
+        if (!out || (!records && record_bytes)) throw std::runtime_error("SHA-256 needs device pointers");
+        if (reinterpret_cast<uintptr_t>(out) % 16) throw std::runtime_error("SHA-256 output must be 16-byte aligned");
+        hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+        const bool aligned = (reinterpret_cast<uintptr_t>(records) % 16 == 0) && (record_pitch % 16 == 0);
+        const unsigned grid = static_cast<unsigned>((n_records + 63) / 64);
+        const auto* base = static_cast<const uint8_t*>(records);
+        auto* words = reinterpret_cast<uint32_t*>(out);
+        if (aligned)
+            hipLaunchKernelGGL(sha256_kernel<true>, dim3(grid), dim3(64), 0, s, base, record_bytes, record_pitch,
+                               n_records, words);
+        else
+            hipLaunchKernelGGL(sha256_kernel<false>, dim3(grid), dim3(64), 0, s, base, record_bytes, record_pitch,
+                               n_records, words);
+        check_launch("sha256");
+    });
+}
+
+}  // extern "C"

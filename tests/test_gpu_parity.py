@@ -1,0 +1,257 @@
+"""HIP kernels against the CPU oracle on the same seeded inputs, at sizes the oracle finishes in seconds.
+
+Bit-exact throughout: records, restored caches, CRC32C and SHA-256 (the
+reference compares bit for bit too, tests/connector/test_copy_kernel_cuda.py:63).
+"""
+import ctypes as C
+import hashlib
+import random
+
+import numpy as np
+import pytest
+
+torch = pytest.importorskip("torch")
+
+from kvsnap_amd import synth
+from kvsnap_amd.dataplane import TorchBlockDataPlane, _check, digest_device_records, kernel_library
+
+pytestmark = pytest.mark.gpu
+
+LAYERS, BLOCKS, BLOCK_SIZE, HEADS, WIDTH = 6, 96, 16, 8, 256
+
+
+@pytest.fixture
+def planes(hip_library):
+    made = []
+
+    def make(caches, block_size=BLOCK_SIZE, capacity=64 << 20, **kwargs):
+        plane = TorchBlockDataPlane(caches, block_size, capacity, **kwargs)
+        plane.warm_up()
+        made.append(plane)
+        return plane
+
+    yield make
+    torch.cuda.synchronize()
+    for plane in made:
+        plane.close()
+
+
+def vllm_caches(layers, blocks, seed=0):
+    """The reference's GPU fixture: random bf16 bits, [blocks, H, N, 2D] views of [blocks, N, H, 2D] storage."""
+    generator = torch.Generator(device="cuda").manual_seed(seed)
+    backing = torch.randint(-2**15, 2**15, (layers, blocks, BLOCK_SIZE, HEADS, WIDTH), dtype=torch.int16,
+                            device="cuda", generator=generator).view(torch.bfloat16)
+    return backing, {f"model.layers.{i}.self_attn.attn": backing[i].permute(0, 2, 1, 3) for i in range(layers)}
+
+
+def host_copy(backing):
+    torch.cuda.synchronize()
+    return backing.contiguous().view(torch.uint8).cpu().numpy().reshape(-1).copy()
+
+
+def host_spans(plane, backing, host):
+    """The plane's spans re-based onto a host copy of ``backing``."""
+    base = backing.data_ptr()
+    return [(host.ctypes.data + (s[1] - base), s[2], s[0], s[3]) for s in plane.spans()]
+
+
+def pinned_bytes(allocation, offset, size):
+    return np.frombuffer(C.string_at(allocation.pointer + offset, size), dtype=np.uint8)
+
+
+def test_a_saved_snapshot_restores_bit_for_bit_into_shuffled_blocks(planes):
+    """The reference's own GPU case (test_copy_kernel_cuda.py:41-63), on the HIP kernels."""
+    backing, caches = vllm_caches(LAYERS, BLOCKS)
+    plane = planes(caches)
+    rng = random.Random(1)
+    saved = rng.sample(range(1, BLOCKS), 20)
+    restored = rng.sample([b for b in range(1, BLOCKS) if b not in saved], 20)
+    size = plane.block_bytes
+    before = backing.view(torch.int16).clone()
+    for kind in ("staging", "per-block"):
+        owned = ([plane.pool.reserve(size * len(saved))] if kind == "staging"
+                 else [plane.pool.reserve(size) for _ in saved])
+        targets = ([(owned[0], i * size) for i in range(len(saved))] if kind == "staging"
+                   else [(allocation, 0) for allocation in owned])
+        plane.save_gather(saved, targets, len(saved) * BLOCK_SIZE)
+        progress = []
+        assert plane.load_scatter(restored, targets, progress=progress, chunk_bytes=3 * size) == 7
+        assert all(event.query() for event, _ in progress[1:])
+        torch.cuda.synchronize()
+        after = backing.view(torch.int16).clone()
+        expected = before.clone()
+        expected[:, restored] = before[:, saved]
+        assert torch.equal(after, expected), kind
+        backing.view(torch.int16).copy_(before)
+        for allocation in owned:
+            allocation.close()
+
+
+@pytest.mark.parametrize("layout", ["vllm", "kv_split"])
+@pytest.mark.parametrize("kind", [synth.KIND_BF16, synth.KIND_E4M3, synth.KIND_BYTES])
+def test_synthetic_fill_matches_the_oracle_generator(planes, oracle_lib, layout, kind):
+    dtype = torch.float8_e4m3fn if kind == synth.KIND_E4M3 else torch.bfloat16
+    caches, backing = synth.make_caches(3, 8, layout=layout, dtype=dtype)
+    plane = planes(caches)
+    scales = [0.5 + 0.25 * i for i in range(len(plane.spans()))] if kind == synth.KIND_E4M3 else None
+    keep = synth.fill(plane, 1234, kind=kind, inv_scales=scales)
+    host = host_copy(backing)
+    del keep
+    for index, (host_addr, pitch, _, nbytes) in enumerate(host_spans(plane, backing, host)):
+        for block in range(8):
+            start = host_addr - host.ctypes.data + block * pitch
+            got = host[start:start + nbytes]
+            expected = oracle_lib.fill_span(1234, index, block, nbytes, kind, scales[index] if scales else 1.0)
+            assert np.array_equal(got, expected), (index, block)
+
+
+@pytest.mark.parametrize("layout", ["vllm", "kv_split"])
+def test_save_gather_matches_the_oracle_records_and_zeroes_the_tail(planes, oracle_lib, layout):
+    caches, backing = synth.make_caches(LAYERS, 24, layout=layout)
+    plane = planes(caches)
+    keep = synth.fill(plane, 5, kind=synth.KIND_BYTES)
+    host = host_copy(backing)
+    del keep
+    block_ids, tokens = [7, 2, 9, 3, 4], 4 * BLOCK_SIZE + 5
+    size = plane.block_bytes
+    records = oracle_lib.gather(host_spans(plane, backing, host), block_ids, size)
+    oracle_lib.zero_tail(records[-1], plane.layers, 5)
+    for kind, copies in (("per-block", 5), ("staging", 3)):
+        owned = ([plane.pool.reserve(size * len(block_ids))] if kind == "staging"
+                 else [plane.pool.reserve(size) for _ in block_ids])
+        targets = ([(owned[0], i * size) for i in range(len(block_ids))] if kind == "staging"
+                   else [(allocation, 0) for allocation in owned])
+        assert plane.save_gather(block_ids, targets, tokens, chunk_bytes=2 * size) == copies
+        for index, (allocation, offset) in enumerate(targets):
+            assert np.array_equal(pinned_bytes(allocation, offset, size), records[index]), (kind, index)
+        assert np.array_equal(host_copy(backing), host), "the KV cache is only read"
+        for allocation in owned:
+            allocation.close()
+
+
+def test_gpu_digests_match_the_oracle_and_hashlib(planes, oracle_lib):
+    caches, backing = synth.make_caches(LAYERS, 40, layout="vllm")
+    plane = planes(caches)
+    keep = synth.fill(plane, 9)
+    torch.cuda.synchronize()
+    del keep
+    block_ids = random.Random(3).sample(range(1, 40), 17)
+    tokens = 16 * 16 + 3
+    size = plane.block_bytes
+    staged = plane.pool.reserve(size * len(block_ids))
+    targets = [(staged, i * size) for i in range(len(block_ids))]
+    digests = []
+    plane.save_gather(block_ids, targets, tokens, digests=digests)
+    got = digests[0].result()
+    for index, (hexdigest, crc) in enumerate(got):
+        record = C.string_at(staged.pointer + index * size, size)
+        assert crc == oracle_lib.crc32c(record), index
+        assert hexdigest == hashlib.sha256(record).hexdigest() == oracle_lib.sha256(record).hex(), index
+    staged.close()
+
+
+@pytest.mark.parametrize("record_bytes", [0, 1, 5, 16, 63, 64, 65, 119, 120, 192, 4095, 4096, 4097, 65520,
+                                          65536, 65552, 200000, 2 * 65536 + 48])
+def test_crc32c_and_sha256_kernels_on_odd_record_sizes(hip_library, oracle_lib, record_bytes):
+    n = 5
+    for pitch in {record_bytes, record_bytes + (-record_bytes % 16), record_bytes + 24}:
+        pitch = max(pitch, 1)
+        data = torch.randint(0, 256, (n * pitch + 16,), dtype=torch.uint8, device="cuda")
+        for shift in (0, 8, 3):
+            stream = torch.cuda.current_stream()
+            crc, sha, workspace = digest_device_records(torch, data.data_ptr() + shift, record_bytes, pitch, n,
+                                                        data.device, stream)
+            torch.cuda.synchronize()
+            host = data.cpu().numpy()
+            for r in range(n):
+                rec = host[shift + r * pitch: shift + r * pitch + record_bytes].tobytes()
+                assert (int(crc[r]) & 0xFFFFFFFF) == oracle_lib.crc32c(rec), (record_bytes, pitch, shift, r)
+                assert bytes(sha[r].cpu().numpy()) == hashlib.sha256(rec).digest(), (record_bytes, pitch, shift, r)
+            del workspace
+
+
+def test_crc32c_kernel_extends_a_prior_value(hip_library, oracle_lib):
+    lib = kernel_library()
+    data = torch.randint(0, 256, (3 * 70000,), dtype=torch.uint8, device="cuda")
+    out = torch.zeros(3, dtype=torch.int32, device="cuda")
+    work_bytes = lib.kvsnap_crc32c_workspace_bytes(70000, 3)
+    work = torch.empty(work_bytes, dtype=torch.uint8, device="cuda")
+    for prior in (0, 1, 0xE3069283, 0xFFFFFFFF):
+        _check(lib, lib.kvsnap_crc32c_records(data.data_ptr(), 70000, 70000, 3, prior, out.data_ptr(),
+                                              work.data_ptr(), work_bytes, torch.cuda.current_stream().cuda_stream))
+        torch.cuda.synchronize()
+        host = data.cpu().numpy()
+        for r in range(3):
+            assert (int(out[r]) & 0xFFFFFFFF) == oracle_lib.crc32c(host[r * 70000:(r + 1) * 70000].tobytes(), prior)
+
+
+@pytest.mark.parametrize("strides", [(96, 32, 8, 1), (96, 8, 24, 1), (192, 32, 8, 1), (192, 8, 24, 1)])
+def test_tail_zeroing_and_restore_follow_the_actual_strides(planes, strides):
+    """The reference's stride permutations (test_scatter_gather.py:291-317) through the HIP kernels."""
+    shape = (5, 3, 4, 8)
+    storage = torch.arange(5 * strides[0], dtype=torch.int16, device="cuda").view(torch.bfloat16)
+    cache = storage.as_strided(shape, strides)
+    plane = planes({"layer.0": cache}, block_size=4, capacity=1 << 20)
+    before = storage.clone()
+    owned = [plane.pool.reserve(plane.block_bytes) for _ in range(2)]
+    targets = [(allocation, 0) for allocation in owned]
+    plane.save_gather([1, 3], targets, 6)
+    for index, block in enumerate((1, 3)):
+        span = before[block * strides[0]:block * strides[0] + 96].view(torch.int16).clone()
+        if index == 1:
+            for head in range(3):
+                for token in (2, 3):
+                    start = head * strides[1] + token * strides[2]
+                    span[start:start + 8] = 0
+        got = np.frombuffer(C.string_at(owned[index].pointer, 192), dtype=np.int16)
+        assert np.array_equal(got, span.cpu().numpy())
+    assert torch.equal(storage.view(torch.int16), before.view(torch.int16))
+    plane.load_scatter([0, 4], targets)
+    torch.cuda.synchronize()
+    expected = before.view(torch.int16).clone()
+    for block, allocation in zip((0, 4), owned):
+        payload = torch.from_numpy(np.frombuffer(C.string_at(allocation.pointer, 192), dtype=np.int16).copy())
+        expected[block * strides[0]:block * strides[0] + 96] = payload.cuda()
+    assert torch.equal(storage.view(torch.int16), expected)
+    for allocation in owned:
+        allocation.close()
+
+
+def test_kv_split_layout_round_trips_through_pinned_records(planes, oracle_lib):
+    caches, backing = synth.make_caches(4, 32, layout="kv_split")
+    plane = planes(caches)
+    keep = synth.fill(plane, 77)
+    host = host_copy(backing)
+    del keep
+    saved, restored = synth.block_tables(32, 10)
+    size = plane.block_bytes
+    staged = plane.pool.reserve(size * 10)
+    targets = [(staged, i * size) for i in range(10)]
+    plane.save_gather(saved, targets, 10 * BLOCK_SIZE)
+    records = oracle_lib.gather(host_spans(plane, backing, host), saved, size)
+    assert np.array_equal(pinned_bytes(staged, 0, 10 * size), records.reshape(-1))
+    assert plane.load_scatter(restored, targets) == 1
+    after = host_copy(backing)
+    expected = host.copy()
+    oracle_lib.scatter(host_spans(plane, backing, expected), restored,
+                       [staged.pointer + i * size for i in range(10)])
+    assert np.array_equal(after, expected)
+    staged.close()
+
+
+def test_restore_from_device_memory_uses_the_same_kernel(planes):
+    """Sources may be device addresses (a staged H2D copy) as well as pinned host addresses."""
+    backing, caches = vllm_caches(3, 16, seed=4)
+    plane = planes(caches)
+    size = plane.block_bytes
+    records = torch.randint(-2**15, 2**15, (4, size // 2), dtype=torch.int16, device="cuda")
+    tables = plane._load_tables()
+    from kvsnap_amd.dataplane import copy_host_blocks
+    sources = torch.tensor([records[i].data_ptr() for i in range(4)], dtype=torch.int64, device="cuda")
+    blocks = torch.tensor([3, 9, 1, 14], dtype=torch.int64, device="cuda")
+    copy_host_blocks(sources, blocks, *tables)
+    torch.cuda.synchronize()
+    for i, block in enumerate([3, 9, 1, 14]):
+        for layer, name in enumerate(sorted(caches)):
+            span = caches[name][block].permute(1, 0, 2).contiguous().view(torch.int16).reshape(-1)
+            assert torch.equal(span, records[i][layer * 32768:(layer + 1) * 32768])
