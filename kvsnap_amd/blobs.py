@@ -1,0 +1,135 @@
+"""Snapshot blob files: the on-disk record format and the disk-staged read path.
+
+Format (reference ``kvsnap/store/common.py:10-11``, ``kvsnap/store/blobs.py:94-111``):
+a 32-byte little-endian header ``<8sIQI8s`` = (b"KVSBLOB1", version 1, payload
+length, CRC32C of the payload, 8 zero bytes), then the payload.  A blob's file
+name is its payload's SHA-256 in lowercase hex plus ``.blob``; files are
+written to a temporary name, optionally fdatasync'ed, and renamed.
+
+``read_prepared_into`` is the restore's disk stage (reference
+``kvsnap/store/store.py:686-723``): block ``first_block + i`` is pread into
+``address + i * block_bytes`` of a pinned buffer, by ``workers`` threads,
+under a shared lock on ``<root>/.blob.lock``.  Every block's CRC32C is checked
+against its segment before the caller copies anything to the GPU -- on the
+host (the reference's way) or, with ``verify="none"``, left to the caller's
+GPU check (see ``TorchBlockDataPlane.load_scatter_verified``).
+"""
+from __future__ import annotations
+
+from concurrent.futures import ThreadPoolExecutor
+import fcntl
+import os
+from pathlib import Path
+import struct
+import uuid
+
+from .native_io import get_io_backend
+
+HEADER = struct.Struct("<8sIQI8s")
+MAGIC = b"KVSBLOB1"
+VERSION = 1
+
+
+class CorruptSnapshotError(RuntimeError):
+    """A blob is missing, truncated, or fails its checksum; nothing was copied to the GPU."""
+
+
+def pack_header(length: int, crc32c: int) -> bytes:
+    return HEADER.pack(MAGIC, VERSION, length, crc32c, b"\0" * 8)
+
+
+def parse_header(raw: bytes):
+    """(payload length, CRC32C) of a header, or CorruptSnapshotError."""
+    if len(raw) != HEADER.size:
+        raise CorruptSnapshotError("truncated blob header")
+    magic, version, length, checksum, reserved = HEADER.unpack(raw)
+    if magic != MAGIC or version != VERSION or reserved != b"\0" * 8:
+        raise CorruptSnapshotError("invalid blob header")
+    return length, checksum
+
+
+class BlobDirectory:
+    """The blob files under ``<root>/blobs``, written and read through one I/O backend."""
+
+    def __init__(self, root, *, io_backend=None):
+        self.root = Path(root)
+        self.blob_dir = self.root / "blobs"
+        self.blob_dir.mkdir(parents=True, exist_ok=True)
+        self.io = get_io_backend(io_backend)
+
+    def path(self, blob_id: str) -> Path:
+        if len(blob_id) != 64 or any(c not in "0123456789abcdef" for c in blob_id):
+            raise CorruptSnapshotError("invalid blob identifier")
+        return self.blob_dir / (blob_id + ".blob")
+
+    def write_blob(self, blob_id, data, crc32c, *, durable=False):
+        """Write one blob unless a file of that name already exists (content-addressed dedup)."""
+        final = self.path(blob_id)
+        if final.exists():
+            with final.open("rb") as stream:
+                length, checksum = parse_header(stream.read(HEADER.size))
+            if length != len(data) or checksum != crc32c:
+                raise CorruptSnapshotError("existing blob differs from its content id")
+            return False
+        temporary = self.blob_dir / f"{blob_id}.{uuid.uuid4().hex}.tmp"
+        fd = os.open(temporary, os.O_CREAT | os.O_EXCL | os.O_WRONLY, 0o600)
+        try:
+            self.io.pwrite_all(fd, pack_header(len(data), crc32c), 0)
+            self.io.pwrite_all(fd, data, HEADER.size)
+            if durable:
+                os.fdatasync(fd)
+        finally:
+            os.close(fd)
+        os.replace(temporary, final)
+        return True
+
+    def write_blocks(self, blocks, digests, *, durable=False, workers=8):
+        """Write each block under its (sha256 hex, crc32c); returns the segments, one per block."""
+        if len(blocks) != len(digests):
+            raise ValueError("one digest per block is required")
+        unique = {}
+        for data, (blob_id, crc) in zip(blocks, digests):
+            unique.setdefault(blob_id, (data, crc))
+        with ThreadPoolExecutor(max_workers=workers, thread_name_prefix="kvsnap-write") as pool:
+            list(pool.map(lambda item: self.write_blob(item[0], item[1][0], item[1][1], durable=durable),
+                          unique.items()))
+        if durable:
+            fd = os.open(self.blob_dir, os.O_RDONLY | os.O_DIRECTORY)
+            try:
+                os.fsync(fd)
+            finally:
+                os.close(fd)
+        return [dict(blob_id=blob_id, offset=0, length=len(data), first_block=index, nblocks=1, crc32c=crc)
+                for index, (data, (blob_id, crc)) in enumerate(zip(blocks, digests))]
+
+    def read_prepared_into(self, segments, address, block_bytes, *, first_block=0, workers=8, verify="host"):
+        """pread blocks into packed pinned memory; with ``verify="host"`` CRC-check each one there."""
+        if verify not in ("host", "none"):
+            raise ValueError("verify must be host or none")
+        for index, segment in enumerate(segments, start=first_block):
+            if segment["first_block"] != index or segment["nblocks"] != 1:
+                raise CorruptSnapshotError("noncontiguous prepared block mapping")
+            offset, length = segment["offset"], segment["length"]
+            if type(offset) is not int or type(length) is not int or offset < 0 or length != block_bytes:
+                raise CorruptSnapshotError("prepared segment does not match the KV block size")
+
+        def read(item):
+            index, segment = item
+            target = address + index * block_bytes
+            offset, length = segment["offset"], segment["length"]
+            try:
+                with self.path(segment["blob_id"]).open("rb") as stream:
+                    fd = stream.fileno()
+                    size, _ = parse_header(os.pread(fd, HEADER.size, 0))
+                    if offset + length > size:
+                        raise CorruptSnapshotError("invalid blob header or segment bounds")
+                    self.io.pread_into(fd, target, length, HEADER.size + offset)
+            except (OSError, struct.error) as exc:
+                raise CorruptSnapshotError(f"unreadable blob {segment['blob_id']}: {exc}") from exc
+            if verify == "host" and self.io.crc32c_at(target, length) != segment["crc32c"]:
+                raise CorruptSnapshotError("prepared segment checksum mismatch")
+
+        with (self.root / ".blob.lock").open("a+b") as lock_file:
+            fcntl.flock(lock_file, fcntl.LOCK_SH)
+            with ThreadPoolExecutor(max_workers=workers, thread_name_prefix="kvsnap-read") as pool:
+                list(pool.map(read, enumerate(segments)))

@@ -307,6 +307,19 @@ __global__ __launch_bounds__(64) void crc_combine_kernel(const uint32_t* __restr
 }
 
 // ----------------------------------------------------------------- SHA-256 (FIPS 180-4)
+//
+// SHA-256 is a sequential chain of 64-byte compressions within a record, so
+// records are the only parallelism: one record per lane.  A wave issues one
+// VALU instruction per 4 cycles, so a record's time is its instruction count;
+// everything that does not depend on the chaining state is moved off the
+// wave that runs the rounds:
+//   * a producer wave loads each block, byte-swaps it, expands the message
+//     schedule and adds the round constants (W[t] + K[t]) into LDS, one block
+//     ahead of
+//   * the round wave, which runs only the 64 rounds (about 14 VALU each).
+// Three-input XORs and Maj are single v_bitop3_b32 instructions (truth tables
+// 0x96 and 0xE8, both symmetric in their inputs).  Workgroup = one round wave
+// + one producer wave over the same 64 records.
 
 __constant__ uint32_t kSha[64] = {
     0x428a2f98, 0x71374491, 0xb5c0fbcf, 0xe9b5dba5, 0x3956c25b, 0x59f111f1, 0x923f82a4, 0xab1c5ed5,
@@ -320,103 +333,140 @@ __constant__ uint32_t kSha[64] = {
 };
 
 __device__ __forceinline__ uint32_t rotr(uint32_t x, int n) { return (x >> n) | (x << (32 - n)); }
-
-// w[0..15] are the block's big-endian message words.
-__device__ __forceinline__ void sha_compress(uint32_t h[8], uint32_t w[16]) {
-    uint32_t a = h[0], b = h[1], c = h[2], d = h[3], e = h[4], f = h[5], g = h[6], hh = h[7];
-#pragma unroll
-    for (int t = 0; t < 64; ++t) {
-        uint32_t wt;
-        if (t < 16) {
-            wt = w[t];
-        } else {
-            const uint32_t x15 = w[(t - 15) & 15], x2 = w[(t - 2) & 15];
-            const uint32_t s0 = rotr(x15, 7) ^ rotr(x15, 18) ^ (x15 >> 3);
-            const uint32_t s1 = rotr(x2, 17) ^ rotr(x2, 19) ^ (x2 >> 10);
-            wt = w[t & 15] + s0 + w[(t - 7) & 15] + s1;
-            w[t & 15] = wt;
-        }
-        const uint32_t t1 = hh + (rotr(e, 6) ^ rotr(e, 11) ^ rotr(e, 25)) + ((e & f) | (~e & g)) + kSha[t] + wt;
-        const uint32_t ab = a ^ b;
-        const uint32_t t2 = (rotr(a, 2) ^ rotr(a, 13) ^ rotr(a, 22)) + ((ab & c) | (~ab & b));
-        hh = g; g = f; f = e; e = d + t1; d = c; c = b; b = a; a = t1 + t2;
-    }
-    h[0] += a; h[1] += b; h[2] += c; h[3] += d; h[4] += e; h[5] += f; h[6] += g; h[7] += hh;
+__device__ __forceinline__ uint32_t xor3(uint32_t a, uint32_t b, uint32_t c) {
+    return __builtin_amdgcn_bitop3_b32(a, b, c, 0x96);
 }
-
+__device__ __forceinline__ uint32_t maj3(uint32_t a, uint32_t b, uint32_t c) {
+    return __builtin_amdgcn_bitop3_b32(a, b, c, 0xE8);
+}
 __device__ __forceinline__ uint32_t bswap(uint32_t x) { return __builtin_bswap32(x); }
 
-// One record per lane; a wave hashes 64 records side by side.
+constexpr int kShaBlockQuads = 16;  // 64 schedule words per block, read 4 at a time
+
+// Block `blk` of a record as 16 big-endian words, FIPS 180-4 padding included:
+// blocks [0, whole) are payload, then 1 or 2 final blocks carry the tail,
+// 0x80, zeros and the 64-bit bit length.
 template <bool kAligned>
-__global__ __launch_bounds__(64) void sha256_kernel(const uint8_t* __restrict__ records, uint64_t record_bytes,
-                                                    uint64_t pitch, int64_t n_records, uint32_t* __restrict__ out) {
-    const int64_t r = static_cast<int64_t>(blockIdx.x) * 64 + threadIdx.x;
-    if (r >= n_records) return;
-    const uint8_t* p = records + r * pitch;
-    uint32_t h[8] = {0x6a09e667, 0xbb67ae85, 0x3c6ef372, 0xa54ff53a, 0x510e527f, 0x9b05688c, 0x1f83d9ab, 0x5be0cd19};
-    const uint64_t whole = record_bytes / 64;
-    uint32_t w[16];
-    if (kAligned) {
-        const u32x4* q = reinterpret_cast<const u32x4*>(p);
-        u32x4 cur[4];
-        if (whole) {
-#pragma unroll
-            for (int i = 0; i < 4; ++i) cur[i] = q[i];
-        }
-        for (uint64_t blk = 0; blk < whole; ++blk) {
-            u32x4 nxt[4];
-            const u32x4* nq = q + 4 * (blk + 1 < whole ? blk + 1 : blk);
-#pragma unroll
-            for (int i = 0; i < 4; ++i) nxt[i] = nq[i];
+__device__ __forceinline__ void sha_message(const uint8_t* __restrict__ p, uint64_t record_bytes, uint64_t whole,
+                                            int nfinal, uint64_t blk, uint32_t w[16]) {
+    if (blk < whole) {
+        const uint8_t* bp = p + 64 * blk;
+        if (kAligned) {
+            const u32x4* q = reinterpret_cast<const u32x4*>(bp);
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                w[4 * i] = bswap(cur[i].x);
-                w[4 * i + 1] = bswap(cur[i].y);
-                w[4 * i + 2] = bswap(cur[i].z);
-                w[4 * i + 3] = bswap(cur[i].w);
+                const u32x4 v = q[i];
+                w[4 * i] = bswap(v.x);
+                w[4 * i + 1] = bswap(v.y);
+                w[4 * i + 2] = bswap(v.z);
+                w[4 * i + 3] = bswap(v.w);
             }
-            sha_compress(h, w);
-#pragma unroll
-            for (int i = 0; i < 4; ++i) cur[i] = nxt[i];
-        }
-    } else {
-        for (uint64_t blk = 0; blk < whole; ++blk) {
-            const uint8_t* bp = p + 64 * blk;
+        } else {
 #pragma unroll
             for (int i = 0; i < 16; ++i)
                 w[i] = static_cast<uint32_t>(bp[4 * i]) << 24 | static_cast<uint32_t>(bp[4 * i + 1]) << 16 |
                        static_cast<uint32_t>(bp[4 * i + 2]) << 8 | static_cast<uint32_t>(bp[4 * i + 3]);
-            sha_compress(h, w);
         }
+        return;
     }
-    // Final block(s): the rest of the record, 0x80, zeros, 64-bit bit length.
     const uint64_t rest = record_bytes - 64 * whole;
     const uint8_t* tail = p + 64 * whole;
-    const int nfinal = rest + 9 <= 64 ? 1 : 2;
     const uint64_t bits = record_bytes * 8;
-    for (int f = 0; f < nfinal; ++f) {
-#pragma unroll
-        for (int i = 0; i < 16; ++i) {
-            uint32_t word = 0;
-#pragma unroll
-            for (int k = 0; k < 4; ++k) {
-                const uint64_t pos = static_cast<uint64_t>(64 * f + 4 * i + k);
-                uint32_t byte = 0;
-                if (pos < rest)
-                    byte = tail[pos];
-                else if (pos == rest)
-                    byte = 0x80;
-                else if (pos >= static_cast<uint64_t>(64 * nfinal - 8))
-                    byte = static_cast<uint32_t>(bits >> (8 * (64 * nfinal - 1 - pos))) & 0xFF;
-                word |= byte << (24 - 8 * k);
-            }
-            w[i] = word;
+    const int f = static_cast<int>(blk - whole);
+    for (int i = 0; i < 16; ++i) {
+        uint32_t word = 0;
+        for (int k = 0; k < 4; ++k) {
+            const uint64_t pos = static_cast<uint64_t>(64 * f + 4 * i + k);
+            uint32_t byte = 0;
+            if (pos < rest)
+                byte = tail[pos];
+            else if (pos == rest)
+                byte = 0x80;
+            else if (pos >= static_cast<uint64_t>(64 * nfinal - 8))
+                byte = static_cast<uint32_t>(bits >> (8 * (64 * nfinal - 1 - pos))) & 0xFF;
+            word |= byte << (24 - 8 * k);
         }
-        sha_compress(h, w);
+        w[i] = word;
     }
-    u32x4* o = reinterpret_cast<u32x4*>(out + 8 * r);
-    o[0] = u32x4{bswap(h[0]), bswap(h[1]), bswap(h[2]), bswap(h[3])};
-    o[1] = u32x4{bswap(h[4]), bswap(h[5]), bswap(h[6]), bswap(h[7])};
+}
+
+// Producer: W[t] + K[t] for t = 0..63 into one LDS slot, [quad][lane].
+__device__ __forceinline__ void sha_schedule(uint32_t w[16], u32x4 (*slot)[64], int lane) {
+#pragma unroll
+    for (int q = 0; q < kShaBlockQuads; ++q) {
+        uint32_t v[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int t = 4 * q + i;
+            uint32_t wt;
+            if (t < 16) {
+                wt = w[t];
+            } else {
+                const uint32_t x15 = w[(t - 15) & 15], x2 = w[(t - 2) & 15];
+                const uint32_t s0 = xor3(rotr(x15, 7), rotr(x15, 18), x15 >> 3);
+                const uint32_t s1 = xor3(rotr(x2, 17), rotr(x2, 19), x2 >> 10);
+                wt = w[t & 15] + s0 + w[(t - 7) & 15] + s1;
+                w[t & 15] = wt;
+            }
+            v[i] = wt + kSha[t];
+        }
+        slot[q][lane] = u32x4{v[0], v[1], v[2], v[3]};
+    }
+}
+
+// Round wave: the 64 rounds of one block from its LDS slot.
+__device__ __forceinline__ void sha_rounds(uint32_t h[8], const u32x4 (*slot)[64], int lane) {
+    uint32_t a = h[0], b = h[1], c = h[2], d = h[3], e = h[4], f = h[5], g = h[6], hh = h[7];
+#pragma unroll
+    for (int q = 0; q < kShaBlockQuads; ++q) {
+        const u32x4 wk = slot[q][lane];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const uint32_t k = i == 0 ? wk.x : i == 1 ? wk.y : i == 2 ? wk.z : wk.w;
+            const uint32_t t1 = hh + xor3(rotr(e, 6), rotr(e, 11), rotr(e, 25)) + ((e & f) | (~e & g)) + k;
+            const uint32_t t2 = xor3(rotr(a, 2), rotr(a, 13), rotr(a, 22)) + maj3(a, b, c);
+            hh = g; g = f; f = e; e = d + t1; d = c; c = b; b = a; a = t1 + t2;
+        }
+    }
+    h[0] += a; h[1] += b; h[2] += c; h[3] += d; h[4] += e; h[5] += f; h[6] += g; h[7] += hh;
+}
+
+template <bool kAligned>
+__global__ __launch_bounds__(128) void sha256_kernel(const uint8_t* __restrict__ records, uint64_t record_bytes,
+                                                     uint64_t pitch, int64_t n_records, uint32_t* __restrict__ out) {
+    __shared__ u32x4 sched[2][kShaBlockQuads][64];
+    const int lane = threadIdx.x & 63;
+    const bool producer = threadIdx.x >= 64;
+    const int64_t r = static_cast<int64_t>(blockIdx.x) * 64 + lane;
+    const bool live = r < n_records;
+    // Lanes past the last record hash record 0 (in bounds) and store nothing.
+    const uint8_t* p = records + (live ? r : 0) * pitch;
+    const uint64_t whole = record_bytes / 64;
+    const int nfinal = record_bytes - 64 * whole + 9 <= 64 ? 1 : 2;
+    const uint64_t nblocks = whole + nfinal;
+    uint32_t w[16];
+    if (producer) {
+        sha_message<kAligned>(p, record_bytes, whole, nfinal, 0, w);
+        sha_schedule(w, sched[0], lane);
+    }
+    __syncthreads();
+    uint32_t h[8] = {0x6a09e667, 0xbb67ae85, 0x3c6ef372, 0xa54ff53a, 0x510e527f, 0x9b05688c, 0x1f83d9ab, 0x5be0cd19};
+    for (uint64_t blk = 0; blk < nblocks; ++blk) {
+        if (producer) {
+            if (blk + 1 < nblocks) {
+                sha_message<kAligned>(p, record_bytes, whole, nfinal, blk + 1, w);
+                sha_schedule(w, sched[(blk + 1) & 1], lane);
+            }
+        } else {
+            sha_rounds(h, sched[blk & 1], lane);
+        }
+        __syncthreads();
+    }
+    if (!producer && live) {
+        u32x4* o = reinterpret_cast<u32x4*>(out + 8 * r);
+        o[0] = u32x4{bswap(h[0]), bswap(h[1]), bswap(h[2]), bswap(h[3])};
+        o[1] = u32x4{bswap(h[4]), bswap(h[5]), bswap(h[6]), bswap(h[7])};
+    }
 }
 
 // ----------------------------------------------------------------- host helpers
@@ -612,10 +662,10 @@ int kvsnap_sha256_records(const void* records, uint64_t record_bytes, uint64_t r
         const auto* base = static_cast<const uint8_t*>(records);
         auto* words = reinterpret_cast<uint32_t*>(out);
         if (aligned)
-            hipLaunchKernelGGL(sha256_kernel<true>, dim3(grid), dim3(64), 0, s, base, record_bytes, record_pitch,
+            hipLaunchKernelGGL(sha256_kernel<true>, dim3(grid), dim3(128), 0, s, base, record_bytes, record_pitch,
                                n_records, words);
         else
-            hipLaunchKernelGGL(sha256_kernel<false>, dim3(grid), dim3(64), 0, s, base, record_bytes, record_pitch,
+            hipLaunchKernelGGL(sha256_kernel<false>, dim3(grid), dim3(128), 0, s, base, record_bytes, record_pitch,
                                n_records, words);
         check_launch("sha256");
     });

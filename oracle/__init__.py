@@ -72,6 +72,7 @@ def lib():
             "oracle_crc32c_bitwise": ([C.c_void_p, C.c_size_t, C.c_uint32], C.c_uint32),
             "oracle_crc32c": ([C.c_void_p, C.c_size_t, C.c_uint32], C.c_uint32),
             "oracle_sha256": ([C.c_void_p, C.c_size_t, C.c_void_p], None),
+            "oracle_sha256_select": ([C.c_int], None),
             "oracle_gather": ([C.c_size_t, C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p,
                                C.c_size_t, C.c_void_p, C.c_size_t], None),
             "oracle_scatter": ([C.c_size_t, C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p,
@@ -125,6 +126,11 @@ def sha256(data) -> bytes:
     out = C.create_string_buffer(32)
     lib().oracle_sha256(addr, n, out)
     return out.raw
+
+
+def sha256_select(allow_extensions: bool):
+    """Hash with the portable FIPS 180-4 rounds only (False) or with the CPU's SHA extensions (True)."""
+    lib().oracle_sha256_select(1 if allow_extensions else 0)
 
 
 def digest_records(address: int, record_bytes: int, pitch: int, n: int, *, crc=True, sha=True,

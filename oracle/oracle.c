@@ -15,6 +15,7 @@
 #include <stdint.h>
 #include <string.h>
 #if defined(__x86_64__)
+#include <immintrin.h>
 #include <nmmintrin.h>
 #endif
 
@@ -102,14 +103,70 @@ static void sha_compress(uint32_t h[8], const uint8_t block[64])
     h[0] += a; h[1] += b; h[2] += c; h[3] += d; h[4] += e; h[5] += f; h[6] += g; h[7] += hh;
 }
 
+#if defined(__x86_64__)
+/* The same compression with the x86 SHA extensions (Intel's published
+ * SHA-NI method): state kept as ABEF/CDGH lane pairs, 4 rounds per
+ * sha256rnds2 pair, message schedule by sha256msg1/msg2.  Used for the CPU
+ * baseline; checked against sha_compress and hashlib. */
+__attribute__((target("sha,sse4.1,ssse3")))
+static void sha_compress_ni(uint32_t h[8], const uint8_t *p, size_t blocks)
+{
+    const __m128i bswap = _mm_set_epi64x(0x0c0d0e0f08090a0bLL, 0x0405060700010203LL);
+    __m128i tmp = _mm_shuffle_epi32(_mm_loadu_si128((const __m128i *)&h[0]), 0xB1);
+    __m128i st1 = _mm_shuffle_epi32(_mm_loadu_si128((const __m128i *)&h[4]), 0x1B);
+    __m128i st0 = _mm_alignr_epi8(tmp, st1, 8);
+    st1 = _mm_blend_epi16(st1, tmp, 0xF0);
+    for (; blocks; --blocks, p += 64) {
+        const __m128i save0 = st0, save1 = st1;
+        __m128i m[4];
+        for (int i = 0; i < 4; ++i)
+            m[i] = _mm_shuffle_epi8(_mm_loadu_si128((const __m128i *)(p + 16 * i)), bswap);
+        for (int i = 0; i < 16; ++i) {
+            __m128i wk = _mm_add_epi32(m[i & 3], _mm_loadu_si128((const __m128i *)&SHA_K[4 * i]));
+            st1 = _mm_sha256rnds2_epu32(st1, st0, wk);
+            if (i < 12) {
+                __m128i next = _mm_sha256msg1_epu32(m[i & 3], m[(i + 1) & 3]);
+                next = _mm_add_epi32(next, _mm_alignr_epi8(m[(i + 3) & 3], m[(i + 2) & 3], 4));
+                m[i & 3] = _mm_sha256msg2_epu32(next, m[(i + 3) & 3]);
+            }
+            st0 = _mm_sha256rnds2_epu32(st0, st1, _mm_shuffle_epi32(wk, 0x0E));
+        }
+        st0 = _mm_add_epi32(st0, save0);
+        st1 = _mm_add_epi32(st1, save1);
+    }
+    tmp = _mm_shuffle_epi32(st0, 0x1B);
+    st1 = _mm_shuffle_epi32(st1, 0xB1);
+    _mm_storeu_si128((__m128i *)&h[0], _mm_blend_epi16(tmp, st1, 0xF0));
+    _mm_storeu_si128((__m128i *)&h[4], _mm_alignr_epi8(st1, tmp, 8));
+}
+#endif
+
+static int use_sha_ni = -1;
+
+/* 0: portable rounds only; 1: SHA extensions when the CPU has them. */
+void oracle_sha256_select(int allow_extensions) { use_sha_ni = allow_extensions ? -1 : 0; }
+
+static void sha_blocks(uint32_t h[8], const uint8_t *p, size_t blocks)
+{
+#if defined(__x86_64__)
+    if (use_sha_ni < 0)
+        use_sha_ni = __builtin_cpu_supports("sha") && __builtin_cpu_supports("sse4.1") ? 1 : 0;
+    if (use_sha_ni) {
+        sha_compress_ni(h, p, blocks);
+        return;
+    }
+#endif
+    for (size_t i = 0; i < blocks; ++i)
+        sha_compress(h, p + 64 * i);
+}
+
 void oracle_sha256(const void *data, size_t size, uint8_t out[32])
 {
     uint32_t h[8] = {0x6a09e667, 0xbb67ae85, 0x3c6ef372, 0xa54ff53a,
                      0x510e527f, 0x9b05688c, 0x1f83d9ab, 0x5be0cd19};
     const uint8_t *p = (const uint8_t *)data;
     size_t whole = size / 64;
-    for (size_t i = 0; i < whole; ++i)
-        sha_compress(h, p + 64 * i);
+    sha_blocks(h, p, whole);
     uint8_t tail[128];
     size_t rest = size - 64 * whole;
     memset(tail, 0, sizeof tail);
@@ -119,8 +176,7 @@ void oracle_sha256(const void *data, size_t size, uint8_t out[32])
     uint64_t bits = (uint64_t)size * 8u;
     for (int i = 0; i < 8; ++i)
         tail[64 * blocks - 1 - i] = (uint8_t)(bits >> (8 * i));
-    for (size_t i = 0; i < blocks; ++i)
-        sha_compress(h, tail + 64 * i);
+    sha_blocks(h, tail, blocks);
     for (int i = 0; i < 8; ++i) {
         out[4 * i] = (uint8_t)(h[i] >> 24);
         out[4 * i + 1] = (uint8_t)(h[i] >> 16);
