@@ -1,0 +1,82 @@
+/*
+ * gfx950 kernels of the snapshot dataplane, built into
+ * kvsnap_amd/_native/libkvsnap_hip.so.
+ *
+ * Tables and buffers are device addresses (hipMalloc'd or torch tensors;
+ * `sources` may also be pinned host addresses from the pool, which the restore
+ * kernel reads in place over the host link).  Every entry point launches on
+ * `stream` (a hipStream_t as an integer), returns 0 once the launch is queued
+ * and -1 with kvsnap_cuda_error() set if the arguments are refused or the
+ * launch fails.  Nothing is allocated.
+ *
+ * Span tables: span s of block b lives at span_bases[s] + b * span_pitches[s]
+ * (bytes), is span_words[s] 8-byte words long, and sits at byte
+ * span_offsets[s] of the block's packed record.  One span per layer for the
+ * reference's [blocks, H, N, C] caches (in sorted layer-name order), two per
+ * layer (K, then V) for [2, blocks, N, H, C] caches.
+ */
+#ifndef KVSNAP_KERNELS_H
+#define KVSNAP_KERNELS_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Always 1. */
+int kvsnap_kernels_abi_version(void);
+
+/* Restore: for every (block i, span s), copy span_words[s] words from
+ * sources[i] + span_offsets[s] to span_bases[s] + blocks[i] * span_pitches[s].
+ * `programs` workgroups (<= 0: one per job).  Replaces the Triton launch
+ * copy_host_blocks(sources, blocks, layer_offsets, layer_bases,
+ * layer_pitches, layer_words), kvsnap/connector/copy_kernel.py:43-49
+ * (kernel :22-40), called from kvsnap/connector/dataplane.py:374. */
+int kvsnap_restore_blocks(const int64_t* sources, const int64_t* blocks, int64_t n_blocks,
+                          const int64_t* span_offsets, const int64_t* span_bases, const int64_t* span_pitches,
+                          const int64_t* span_words, int64_t n_spans, int programs, uintptr_t stream);
+
+/* Gather: block blocks[i]'s spans packed into records + i * record_pitch.
+ * Replaces save_gather's torch.cat([raw.index_select(0, ids) ...], out=stage),
+ * kvsnap/connector/dataplane.py:416-417. */
+int kvsnap_gather_blocks(const int64_t* blocks, int64_t n_blocks, const int64_t* span_offsets,
+                         const int64_t* span_bases, const int64_t* span_pitches, const int64_t* span_words,
+                         int64_t n_spans, void* records, int64_t record_pitch, int programs, uintptr_t stream);
+
+/* Zero n byte ranges [base + offsets[i], + lengths[i]): the token slots past
+ * the last computed token of a record.  Replaces the host memsets of
+ * TorchBlockDataPlane._zero_tail, kvsnap/connector/dataplane.py:262-272. */
+int kvsnap_zero_regions(void* base, const int64_t* offsets, const int64_t* lengths, int64_t n, uintptr_t stream);
+
+/* Device bytes of scratch that kvsnap_crc32c_records needs for n records. */
+size_t kvsnap_crc32c_workspace_bytes(uint64_t record_bytes, int64_t n_records);
+
+/* out[i] = CRC32C (Castagnoli, reflected, init/xorout ~0, extending `prior`)
+ * of the record_bytes at records + i * record_pitch.  Bit-exact with
+ * kvsnap_crc32c_extend (csrc/dataplane/io.cpp:39-44); replaces its per-block
+ * host calls at kvsnap/connector/volatile.py:151, kvsnap/store/store.py:622
+ * and :717. */
+int kvsnap_crc32c_records(const void* records, uint64_t record_bytes, uint64_t record_pitch, int64_t n_records,
+                          uint32_t prior, uint32_t* out, void* workspace, size_t workspace_bytes, uintptr_t stream);
+
+/* out[32 * i .. 32 * i + 31] = SHA-256 digest of record i (16-byte aligned
+ * `out`).  Replaces hashlib.sha256(record) at kvsnap/connector/volatile.py:151
+ * and kvsnap/store/store.py:622 (the blob id, blobs.py:33-36). */
+int kvsnap_sha256_records(const void* records, uint64_t record_bytes, uint64_t record_pitch, int64_t n_records,
+                          uint8_t* out, uintptr_t stream);
+
+/* Seeded synthetic KV for benchmarks and tests (no reference counterpart):
+ * every span of blocks [first_block, first_block + n_blocks) filled from a
+ * counter-based generator keyed (seed, span, block, element); kind 0 bf16
+ * ~N(0,1), 1 fp8-e4m3 of N(0,1) * span_inv_scales[s], 2 raw bytes. */
+int kvsnap_synth_fill(uint64_t seed, int kind, const int64_t* span_bases, const int64_t* span_pitches,
+                      const int64_t* span_words, const float* span_inv_scales, int64_t n_spans, int64_t first_block,
+                      int64_t n_blocks, uintptr_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* KVSNAP_KERNELS_H */

@@ -40,16 +40,16 @@ namespace {
 
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 
-constexpr int kThreads = 256;   // copy and CRC workgroups: 4 waves
-constexpr int kUnroll = 8;      // dwordx4 loads in flight per lane in the copy loop
+constexpr int kThreads = 256;   // CRC, zero and synthetic-fill workgroups: 4 waves
 
 // ----------------------------------------------------------------- copies
 
 // Copy nbytes (a multiple of 8; src and dst 8-byte aligned) with the whole
-// workgroup.  The 16-byte path covers everything when both ends are 16-byte
-// aligned, which the host tables normally guarantee.
-__device__ __forceinline__ void copy_span(const char* __restrict__ src, char* __restrict__ dst,
-                                          int64_t nbytes) {
+// workgroup of kT lanes, kU dwordx4 loads in flight per lane.  The 16-byte
+// path covers everything when both ends are 16-byte aligned, which the host
+// tables normally guarantee; an 8-byte tail covers the rest.
+template <int kT, int kU>
+__device__ __forceinline__ void copy_span(const char* __restrict__ src, char* __restrict__ dst, int64_t nbytes) {
     const int tid = threadIdx.x;
     int64_t done = 0;
     if (((reinterpret_cast<uintptr_t>(src) | reinterpret_cast<uintptr_t>(dst)) & 15) == 0) {
@@ -57,25 +57,33 @@ __device__ __forceinline__ void copy_span(const char* __restrict__ src, char* __
         u32x4* d = reinterpret_cast<u32x4*>(dst);
         const int64_t nv = nbytes >> 4;
         int64_t i = tid;
-        for (; i + (kUnroll - 1) * kThreads < nv; i += kUnroll * kThreads) {
-            u32x4 v[kUnroll];
+        for (; i + (kU - 1) * kT < nv; i += kU * kT) {
+            u32x4 v[kU];
 #pragma unroll
-            for (int u = 0; u < kUnroll; ++u) v[u] = __builtin_nontemporal_load(s + i + u * kThreads);
+            for (int u = 0; u < kU; ++u) v[u] = __builtin_nontemporal_load(s + i + u * kT);
 #pragma unroll
-            for (int u = 0; u < kUnroll; ++u) __builtin_nontemporal_store(v[u], d + i + u * kThreads);
+            for (int u = 0; u < kU; ++u) __builtin_nontemporal_store(v[u], d + i + u * kT);
         }
-        for (; i < nv; i += kThreads) __builtin_nontemporal_store(__builtin_nontemporal_load(s + i), d + i);
+        for (; i < nv; i += kT) __builtin_nontemporal_store(__builtin_nontemporal_load(s + i), d + i);
         done = nv << 4;
     }
     const uint64_t* s8 = reinterpret_cast<const uint64_t*>(src + done);
     uint64_t* d8 = reinterpret_cast<uint64_t*>(dst + done);
     const int64_t nw = (nbytes - done) >> 3;
-    for (int64_t i = tid; i < nw; i += kThreads) d8[i] = s8[i];
+    for (int64_t i = tid; i < nw; i += kT) d8[i] = s8[i];
 }
 
-// Job j = (block j / n_spans, span j % n_spans): the reference kernel's
-// order (copy_kernel.py:29-31), so a launch walks its records front to back.
-__global__ __launch_bounds__(kThreads) void restore_kernel(
+// Restore: reads cross the host link, so a small persistent grid of 256-lane
+// workgroups with 8 loads in flight per lane keeps it full while leaving the
+// CUs to the engine.  Job j = (block j / n_spans, span j % n_spans): the
+// reference kernel's order (copy_kernel.py:29-31), so a launch walks its
+// records front to back.
+constexpr int kRestoreThreads = 256, kRestoreUnroll = 8;
+// Gather: HBM to HBM, one 1024-lane workgroup per (block, span) job with 4
+// loads in flight per lane (64 KiB per pass), the fastest shape measured.
+constexpr int kGatherThreads = 1024, kGatherUnroll = 4;
+
+__global__ __launch_bounds__(kRestoreThreads) void restore_kernel(
     const int64_t* __restrict__ sources, const int64_t* __restrict__ blocks, int64_t n_blocks,
     const int64_t* __restrict__ offs, const int64_t* __restrict__ bases, const int64_t* __restrict__ pitches,
     const int64_t* __restrict__ words, int64_t n_spans) {
@@ -84,11 +92,11 @@ __global__ __launch_bounds__(kThreads) void restore_kernel(
         const int64_t b = job / n_spans, s = job - b * n_spans;
         const char* src = reinterpret_cast<const char*>(sources[b] + offs[s]);
         char* dst = reinterpret_cast<char*>(bases[s] + blocks[b] * pitches[s]);
-        copy_span(src, dst, words[s] * 8);
+        copy_span<kRestoreThreads, kRestoreUnroll>(src, dst, words[s] * 8);
     }
 }
 
-__global__ __launch_bounds__(kThreads) void gather_kernel(
+__global__ __launch_bounds__(kGatherThreads) void gather_kernel(
     const int64_t* __restrict__ blocks, int64_t n_blocks, const int64_t* __restrict__ offs,
     const int64_t* __restrict__ bases, const int64_t* __restrict__ pitches, const int64_t* __restrict__ words,
     int64_t n_spans, char* __restrict__ records, int64_t record_pitch) {
@@ -97,7 +105,7 @@ __global__ __launch_bounds__(kThreads) void gather_kernel(
         const int64_t b = job / n_spans, s = job - b * n_spans;
         const char* src = reinterpret_cast<const char*>(bases[s] + blocks[b] * pitches[s]);
         char* dst = records + b * record_pitch + offs[s];
-        copy_span(src, dst, words[s] * 8);
+        copy_span<kGatherThreads, kGatherUnroll>(src, dst, words[s] * 8);
     }
 }
 
@@ -568,7 +576,7 @@ int kvsnap_restore_blocks(const int64_t* sources, const int64_t* blocks, int64_t
         if (n_blocks == 0 || n_spans == 0) return;
         if (!sources || !blocks || !span_offsets || !span_bases || !span_pitches || !span_words)
             throw std::runtime_error("restore tables must be device pointers");
-        hipLaunchKernelGGL(restore_kernel, dim3(grid_for(n_blocks * n_spans, programs)), dim3(kThreads), 0,
+        hipLaunchKernelGGL(restore_kernel, dim3(grid_for(n_blocks * n_spans, programs)), dim3(kRestoreThreads), 0,
                            reinterpret_cast<hipStream_t>(stream), sources, blocks, n_blocks, span_offsets,
                            span_bases, span_pitches, span_words, n_spans);
         check_launch("restore");
@@ -583,7 +591,7 @@ int kvsnap_gather_blocks(const int64_t* blocks, int64_t n_blocks, const int64_t*
         if (n_blocks == 0 || n_spans == 0) return;
         if (!records || !blocks || !span_offsets || !span_bases || !span_pitches || !span_words)
             throw std::runtime_error("gather tables must be device pointers");
-        hipLaunchKernelGGL(gather_kernel, dim3(grid_for(n_blocks * n_spans, programs)), dim3(kThreads), 0,
+        hipLaunchKernelGGL(gather_kernel, dim3(grid_for(n_blocks * n_spans, programs)), dim3(kGatherThreads), 0,
                            reinterpret_cast<hipStream_t>(stream), blocks, n_blocks, span_offsets, span_bases,
                            span_pitches, span_words, n_spans, static_cast<char*>(records), record_pitch);
         check_launch("gather");

@@ -1,0 +1,85 @@
+"""Blob files and the disk-staged read (reference kvsnap/store/blobs.py:78-111, store.py:686-723)."""
+import ctypes as C
+import hashlib
+import os
+import struct
+
+import numpy as np
+import pytest
+
+import oracle
+from kvsnap_amd.blobs import BlobDirectory, CorruptSnapshotError, HEADER, pack_header, parse_header
+
+
+def records(n, size, seed=0):
+    rng = np.random.default_rng(seed)
+    return [rng.integers(0, 256, size, dtype=np.uint8).tobytes() for _ in range(n)]
+
+
+def digests(blocks):
+    return [(hashlib.sha256(b).hexdigest(), oracle.crc32c(b)) for b in blocks]
+
+
+def test_header_is_the_reference_struct_parsed_independently():
+    header = pack_header(1000, 0xDEADBEEF)
+    assert struct.unpack("<8sIQI8s", header) == (b"KVSBLOB1", 1, 1000, 0xDEADBEEF, bytes(8))
+    assert parse_header(header) == (1000, 0xDEADBEEF)
+    for bad in (header[:31], b"KVSBLOB2" + header[8:], header[:8] + struct.pack("<I", 2) + header[12:],
+                header[:24] + b"\x01" + header[25:]):
+        with pytest.raises(CorruptSnapshotError):
+            parse_header(bad)
+
+
+def test_blob_files_match_the_reference_format_and_dedup_by_content(tmp_path):
+    store = BlobDirectory(tmp_path, io_backend="native")
+    blocks = records(4, 4096)
+    blocks.append(blocks[1])                                  # a repeated block is one blob
+    segments = store.write_blocks(blocks, digests(blocks))
+    assert len(list((tmp_path / "blobs").glob("*.blob"))) == 4
+    for block, segment in zip(blocks, segments):
+        raw = (tmp_path / "blobs" / (segment["blob_id"] + ".blob")).read_bytes()
+        magic, version, length, checksum, reserved = HEADER.unpack(raw[:32])
+        assert (magic, version, length, reserved) == (b"KVSBLOB1", 1, 4096, bytes(8))
+        assert raw[32:] == block and checksum == oracle.crc32c(block)
+        assert hashlib.sha256(raw[32:]).hexdigest() == segment["blob_id"]
+    assert [s["first_block"] for s in segments] == list(range(5))
+    assert store.write_blob(segments[0]["blob_id"], blocks[0], segments[0]["crc32c"]) is False
+
+
+def test_read_prepared_into_lands_each_block_in_its_slot_and_checks_crc(tmp_path):
+    store = BlobDirectory(tmp_path, io_backend="native")
+    size = 65536 + 48
+    blocks = records(6, size, seed=3)
+    segments = store.write_blocks(blocks, digests(blocks), durable=True)
+    target = C.create_string_buffer(size * 6)
+    store.read_prepared_into(segments, C.addressof(target), size, workers=3)
+    assert target.raw == b"".join(blocks)
+    # a restore that skips its first blocks: segments from first_block on are
+    # checked against their block index and packed from the buffer's start
+    target2 = C.create_string_buffer(size * 4)
+    store.read_prepared_into(segments[2:], C.addressof(target2), size, first_block=2)
+    assert target2.raw == b"".join(blocks[2:])
+
+
+def test_a_corrupt_or_missing_blob_is_refused_before_any_copy(tmp_path):
+    store = BlobDirectory(tmp_path, io_backend="native")
+    blocks = records(3, 8192, seed=4)
+    segments = store.write_blocks(blocks, digests(blocks))
+    path = tmp_path / "blobs" / (segments[1]["blob_id"] + ".blob")
+    raw = bytearray(path.read_bytes())
+    raw[-1] ^= 1
+    path.write_bytes(bytes(raw))
+    target = C.create_string_buffer(8192 * 3)
+    with pytest.raises(CorruptSnapshotError, match="checksum"):
+        store.read_prepared_into(segments, C.addressof(target), 8192)
+    store.read_prepared_into(segments, C.addressof(target), 8192, verify="none")     # left to a GPU check
+    os.unlink(path)
+    with pytest.raises(CorruptSnapshotError, match="unreadable"):
+        store.read_prepared_into(segments, C.addressof(target), 8192)
+    bad = dict(segments[0], first_block=5)
+    with pytest.raises(CorruptSnapshotError, match="noncontiguous"):
+        store.read_prepared_into([bad], C.addressof(target), 8192)
+    with pytest.raises(CorruptSnapshotError, match="block size"):
+        store.read_prepared_into(segments[:1], C.addressof(target), 4096)
+    with pytest.raises(CorruptSnapshotError, match="identifier"):
+        store.path("../etc/passwd")

@@ -1,0 +1,66 @@
+"""The C-ABI libraries load without a GPU and export every symbol include/*.h declares."""
+import ctypes as C
+import re
+import subprocess
+from pathlib import Path
+
+import pytest
+
+ROOT = Path(__file__).resolve().parents[1]
+HIP_LIBRARY = ROOT / "kvsnap_amd" / "_native" / "libkvsnap_hip.so"
+IO_LIBRARY = ROOT / "kvsnap_amd" / "_native" / "libkvsnap_io.so"
+LIBRARIES = {"kvsnap_pool.h": HIP_LIBRARY, "kvsnap_kernels.h": HIP_LIBRARY, "kvsnap_io.h": IO_LIBRARY}
+
+
+def declared(header):
+    text = re.sub(r"/\*.*?\*/", "", (ROOT / "include" / header).read_text(), flags=re.S)
+    return sorted(set(re.findall(r"\b(kvsnap_\w+)\s*\(", text)))
+
+
+@pytest.fixture(scope="module", autouse=True)
+def built():
+    if not (HIP_LIBRARY.is_file() and IO_LIBRARY.is_file()):
+        from kvsnap_amd import build
+        build.build_all()
+
+
+def test_every_header_declares_something():
+    for header in LIBRARIES:
+        assert len(declared(header)) >= 3, header
+
+
+@pytest.mark.parametrize("header", sorted(LIBRARIES))
+def test_library_exports_every_declared_symbol(header):
+    path = LIBRARIES[header]
+    exported = set(subprocess.run(["nm", "-D", "--defined-only", str(path)], check=True, capture_output=True,
+                                  text=True).stdout.split())
+    missing = [name for name in declared(header) if name not in exported]
+    assert not missing, f"{path.name} lacks {missing}"
+    lib = C.CDLL(str(path))          # loads without touching a GPU
+    for name in declared(header):
+        assert getattr(lib, name)
+
+
+def test_abi_versions_without_a_gpu():
+    hip = C.CDLL(str(HIP_LIBRARY))
+    assert hip.kvsnap_pool_abi_version() == 2
+    assert hip.kvsnap_kernels_abi_version() == 1
+    io = C.CDLL(str(IO_LIBRARY))
+    assert io.kvsnap_io_abi_version() == 1
+
+
+def test_library_resolution_needs_no_gpu(monkeypatch):
+    from kvsnap_amd.dataplane import resolve_cuda_library
+    monkeypatch.delenv("KVSNAP_CUDA_LIBRARY", raising=False)
+    monkeypatch.delenv("KVSNAP_HIP_LIBRARY", raising=False)
+    assert resolve_cuda_library() == HIP_LIBRARY
+    monkeypatch.setenv("KVSNAP_CUDA_LIBRARY", "/tmp/other.so")
+    assert str(resolve_cuda_library()) == "/tmp/other.so"
+    assert str(resolve_cuda_library("/x/y.so")) == "/x/y.so"
+
+
+def test_missing_hip_library_fails_loudly(monkeypatch, tmp_path):
+    from kvsnap_amd import dataplane
+    monkeypatch.setenv("KVSNAP_CUDA_LIBRARY", str(tmp_path / "absent.so"))
+    with pytest.raises(RuntimeError, match="not built"):
+        dataplane.kernel_library()
