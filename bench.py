@@ -1,35 +1,45 @@
 #!/usr/bin/env python
-"""KV snapshot save + restore on one MI355X: an 8192-token Qwen3-8B session.
+"""KV snapshot save + restore on one MI355X.
 
-Workload (one step): save a 512-block session out of a 16384-block paged
-cache (36 layers x {K,V}, 8 KV heads, head_dim 128, block_size 16, bf16
-~N(0,1) from seed 0, block ids seeded) -- GPU gather, DMA into pinned host
-memory, per-block CRC32C and SHA-256 on the GPU -- then restore it from the
-pinned records into a fresh seeded block table with the restore kernel.
-1,207,959,552 bytes each way.
+Default workload (one step): save an 8192-token Qwen3-8B session -- 512
+blocks out of a 16384-block paged cache (36 layers x {K,V}, 8 KV heads,
+head_dim 128, block_size 16, bf16 ~N(0,1) from seed 0, block ids seeded) --
+with the GPU gather, DMA into pinned host memory and per-block CRC32C +
+SHA-256 on the GPU, then restore it from the pinned records into a fresh
+seeded block table with the restore kernel.  1,207,959,552 bytes each way.
 
     python bench.py [--steps K] [--warmup W] [--layout kv_split|vllm]
 
-Prints one JSON line.  ``value`` is the step's snapshot throughput (save
-bytes + restore bytes) / (time per step), with the cache resident in HBM.
-Also reported: save and restore latency and GB/s, the measured contiguous
-pinned<->device DMA peaks and the fractions of them reached, per-kernel HIP
-event durations, the rooflines, and the CPU path on the host's cores.
+prints one JSON line: ``value`` = (save bytes + restore bytes) / time per
+step, with the cache resident in HBM; plus save/restore latency and GB/s, the
+measured pinned<->device DMA peaks and the fractions of them reached,
+early-readiness latency, per-kernel HIP-event durations, the rooflines, and
+the CPU path timed on this host's cores.
+
+Other workloads (one JSON line each, for the record; not the headline):
+    --workload disk-fork      32768-token session saved as blob files with a
+                              forked child sharing its first 1536 blocks, then
+                              the child restored from disk (pread into pinned
+                              staging, CRC32C-verified on the host or the GPU)
+    --workload rotating-fp8   Qwen3-1.7B fp8-e4m3 sessions of 1k/2k/4k/8k tokens
+                              saved and restored round-robin beside a synthetic
+                              16-sequence decode on the compute stream
+    --workload kernels        each kernel alone plus a plain copy of known size
+                              (the driver for rocprofv3 counter runs)
 """
 from __future__ import annotations
 
 import argparse
 import json
 import os
+import random
 import statistics
 import sys
+import tempfile
+import threading
 import time
 
-LAYERS, NUM_BLOCKS, BLOCK_SIZE, HEADS, HEAD_DIM = 36, 16384, 16, 8, 128
-TOKENS = 8192
-SESSION_BLOCKS = TOKENS // BLOCK_SIZE
 HBM_PEAK_GBPS = 8000.0
-EARLY_REPORT_BYTES = 128 << 20
 
 
 def log(*args):
@@ -48,32 +58,44 @@ def median_ms(torch, stream, fn, reps=5):
     return statistics.median(times)
 
 
-def cpu_baseline(seconds_budget=20.0):
+def percentile(values, q):
+    ordered = sorted(values)
+    return ordered[min(len(ordered) - 1, int(round(q / 100 * (len(ordered) - 1))))]
+
+
+def link_peaks(torch, staged, stream, nbytes):
+    """Measured contiguous pinned <-> device DMA rates (GB/s) for one nbytes copy."""
+    buffer = torch.empty(nbytes, dtype=torch.uint8, device="cuda")
+    h2d_ms = median_ms(torch, stream, lambda: staged.copy(buffer.data_ptr(), nbytes, 0, to_host=False))
+    d2h_ms = median_ms(torch, stream, lambda: staged.copy(buffer.data_ptr(), nbytes, 0, to_host=True))
+    return nbytes / h2d_ms / 1e6, nbytes / d2h_ms / 1e6
+
+
+def cpu_baseline(layers, span, seconds_budget=20.0):
     """The reference's CPU path restated by the oracle, on this host's cores.
 
-    Per sample block: gather its 36 spans into a packed record (memcpy),
-    CRC32C (SSE4.2) and SHA-256 (SHA extensions) of the record, and scatter it
-    back into other blocks (memcpy) -- on 1 thread and on min(16, nproc)
-    threads.  Sample: 64 blocks of a 256-block host cache, repeated until
-    about ``seconds_budget`` seconds have passed.
+    Per sample block: gather its spans into a packed record (memcpy), CRC32C
+    (SSE4.2) and SHA-256 (SHA extensions) of the record, and scatter it back
+    into other blocks (memcpy) -- on 1 thread and on min(16, nproc) threads.
+    Sample: 64 blocks of a 256-block host cache, repeated for about
+    ``seconds_budget`` seconds.
     """
     import numpy as np
     import oracle
     oracle.build()
     oracle.sha256_select(True)
     lib = oracle.lib()
-    span = HEADS * 2 * HEAD_DIM * BLOCK_SIZE * 2       # 65536 bytes per (layer, block)
     host_blocks, sample = 256, 64
-    record = LAYERS * span
-    cache = np.frombuffer(np.random.default_rng(0).bytes(LAYERS * host_blocks * span), dtype=np.uint8).copy()
+    record = layers * span
+    cache = np.frombuffer(np.random.default_rng(0).bytes(layers * host_blocks * span), dtype=np.uint8).copy()
     base = cache.ctypes.data
-    span_base = np.array([base + l * host_blocks * span for l in range(LAYERS)], dtype=np.uint64)
-    span_pitch = np.full(LAYERS, span, dtype=np.int64)
-    span_off = np.array([l * span for l in range(LAYERS)], dtype=np.int64)
-    span_len = np.full(LAYERS, span, dtype=np.int64)
-    import random
+    span_base = np.array([base + l * host_blocks * span for l in range(layers)], dtype=np.uint64)
+    span_pitch = np.full(layers, span, dtype=np.int64)
+    span_off = np.array([l * span for l in range(layers)], dtype=np.int64)
+    span_len = np.full(layers, span, dtype=np.int64)
     ids = np.array(random.Random(1).sample(range(1, host_blocks), sample), dtype=np.int64)
-    dst = np.array(random.Random(2).sample([b for b in range(1, host_blocks) if b not in set(ids.tolist())], sample),
+    taken = set(ids.tolist())
+    dst = np.array(random.Random(2).sample([b for b in range(1, host_blocks) if b not in taken], sample),
                    dtype=np.int64)
     records = np.zeros(sample * record, dtype=np.uint8)
     crcs = np.zeros(sample, dtype=np.uint32)
@@ -83,74 +105,73 @@ def cpu_baseline(seconds_budget=20.0):
     result = {}
     for threads in sorted({1, threads_max}):
         reps, elapsed = 0, 0.0
-        deadline = seconds_budget / 2
-        while elapsed < deadline or reps == 0:
+        while elapsed < seconds_budget / 2 or reps == 0:
             t0 = time.perf_counter()
-            lib.oracle_copy_threads(LAYERS, span_base.ctypes.data, span_pitch.ctypes.data, span_off.ctypes.data,
+            lib.oracle_copy_threads(layers, span_base.ctypes.data, span_pitch.ctypes.data, span_off.ctypes.data,
                                     span_len.ctypes.data, ids.ctypes.data, None, sample, records.ctypes.data, record,
                                     threads)
             lib.oracle_digest_records(records.ctypes.data, record, record, sample, crcs.ctypes.data,
                                       shas.ctypes.data, threads)
-            lib.oracle_copy_threads(LAYERS, span_base.ctypes.data, span_pitch.ctypes.data, span_off.ctypes.data,
+            lib.oracle_copy_threads(layers, span_base.ctypes.data, span_pitch.ctypes.data, span_off.ctypes.data,
                                     span_len.ctypes.data, dst.ctypes.data, sources.ctypes.data, sample, None, record,
                                     threads)
             elapsed += time.perf_counter() - t0
             reps += 1
         result[threads] = 2 * sample * record * reps / elapsed / 1e9
-    return {"value": result[threads_max], "unit": "GB/s", "cores": threads_max, "kind": "port",
-            "single_thread_gbps": result[1],
-            "sample": (f"{sample} Qwen3-8B blocks ({sample * record} B) of a {host_blocks}-block host cache: "
-                       "gather + CRC32C + SHA-256 + scatter, repeated ~{:.0f} s".format(seconds_budget))}
+    return {"value": round(result[threads_max], 3), "unit": "GB/s", "cores": threads_max, "kind": "port",
+            "single_thread_gbps": round(result[1], 3),
+            "sample": (f"{sample} blocks x {record} B of a {host_blocks}-block host cache: gather + CRC32C + "
+                       f"SHA-256 + scatter, repeated ~{seconds_budget:.0f} s (save + restore bytes per second)")}
 
 
-def main():
-    parser = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
-    parser.add_argument("--gpus", type=int, default=1)
-    parser.add_argument("--steps", type=int, default=10)
-    parser.add_argument("--warmup", type=int, default=3)
-    parser.add_argument("--layout", choices=("kv_split", "vllm"), default="kv_split")
-    parser.add_argument("--cpu-seconds", type=float, default=20.0)
-    parser.add_argument("--no-cpu-baseline", action="store_true")
-    args = parser.parse_args()
-    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
-        print("bench.py measures one GPU: every GPU saves and restores its own KV shard over its own host link, "
-              "so there is no multi-GPU step to time here (run with --gpus 1)", file=sys.stderr)
-        sys.exit(2)
+def measured_traffic(kernel):
+    """HBM bytes per launch of ``kernel`` from the committed rocprofv3 counter summary
+    (FETCH_SIZE and WRITE_SIZE, each scaled by a plain copy of known size), or None."""
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "qwen3-8b-8k-kernels.traffic.json")
+    try:
+        with open(path) as f:
+            return round(json.load(f)["kernels"][kernel]["traffic_bytes"])
+    except (OSError, KeyError, ValueError):
+        return None
 
+
+def same_blocks(torch, caches, a, b):
+    ia, ib = torch.tensor(a, device="cuda"), torch.tensor(b, device="cuda")
+    return all(torch.equal(t[:, ia].view(torch.int16), t[:, ib].view(torch.int16)) if t.ndim == 5
+               else torch.equal(t[ia].view(torch.int16), t[ib].view(torch.int16)) for t in caches.values())
+
+
+# ---------------------------------------------------------------- default workload
+
+def run_save_restore(args):
     import torch
     from kvsnap_amd import synth
     from kvsnap_amd.dataplane import KernelTimer, TorchBlockDataPlane
+    from kvsnap_amd.ordering import early_launch_index
 
-    torch.cuda.set_device(0)
-    caches, backing = synth.make_caches(LAYERS, NUM_BLOCKS, block_size=BLOCK_SIZE, heads=HEADS, head_dim=HEAD_DIM,
-                                        layout=args.layout)
-    plane = TorchBlockDataPlane(caches, BLOCK_SIZE, SESSION_BLOCKS * LAYERS * 65536 + (64 << 20))
+    layers, num_blocks, block_size, tokens = 36, 16384, 16, 8192
+    session = tokens // block_size
+    caches, backing = synth.make_caches(layers, num_blocks, block_size=block_size, layout=args.layout)
+    plane = TorchBlockDataPlane(caches, block_size, session * layers * 65536 + (64 << 20))
     plane.warm_up()
     keep = synth.fill(plane, 0)
     torch.cuda.synchronize()
     del keep
     size = plane.block_bytes
-    total = SESSION_BLOCKS * size
-    source, target = synth.block_tables(NUM_BLOCKS, SESSION_BLOCKS)
+    total = session * size
+    source, target = synth.block_tables(num_blocks, session)
     staged = plane.pool.reserve(total)
-    targets = [(staged, i * size) for i in range(SESSION_BLOCKS)]
-    stream = plane._copy_stream
-    log(f"setup: {LAYERS} layers x {NUM_BLOCKS} blocks ({args.layout}), record {size} B, session {total} B")
-
-    # Measured link peaks: one contiguous pinned <-> device DMA of the whole session.
-    device_buffer = torch.empty(total, dtype=torch.uint8, device="cuda")
-    h2d_ms = median_ms(torch, stream, lambda: staged.copy(device_buffer.data_ptr(), total, 0, to_host=False))
-    d2h_ms = median_ms(torch, stream, lambda: staged.copy(device_buffer.data_ptr(), total, 0, to_host=True))
-    del device_buffer
-    h2d_peak, d2h_peak = total / h2d_ms / 1e6, total / d2h_ms / 1e6
+    targets = [(staged, i * size) for i in range(session)]
+    log(f"setup: {layers} layers x {num_blocks} blocks ({args.layout}), record {size} B, session {total} B")
+    h2d_peak, d2h_peak = link_peaks(torch, staged, plane._copy_stream, total)
     log(f"DMA peaks: H2D {h2d_peak:.1f} GB/s, D2H {d2h_peak:.1f} GB/s")
 
-    save_ms, hashed_ms, restore_ms, early_ms = [], [], [], []
+    save_ms, hashed_ms, restore_ms = [], [], []
 
     def step(record):
         digests, progress = [], []
         t0 = time.perf_counter()
-        plane.save_gather(source, targets, TOKENS, digests=digests)
+        plane.save_gather(source, targets, tokens, digests=digests)
         t1 = time.perf_counter()
         plane.load_scatter(target, targets, progress=progress)
         t2 = time.perf_counter()
@@ -176,33 +197,26 @@ def main():
     kernels = timer.summary()
     ms_per_step = elapsed * 1e3 / args.steps
 
-    # Early readiness: launch count and how much was still in flight when the
-    # last launch was queued (the connector reports a load once <= 128 MiB remain).
+    # Early readiness: a load may be reported once every launch is queued and at
+    # most 128 MiB remain; time from the first restore launch to the completion
+    # of the launch after which that holds (last step's events).
     launches = len(progress) - 1
+    restore_pairs = timer.pairs["restore"][-launches:]
+    early_ms = restore_pairs[0][0].elapsed_time(restore_pairs[early_launch_index(progress)][1])
+    restore_span_ms = restore_pairs[0][0].elapsed_time(restore_pairs[-1][1])
 
-    # Parity of the last step (outside the timed region): restored blocks equal
-    # the saved ones, and the GPU digests equal the oracle's on the pinned records.
-    src_ids = torch.tensor(source, device="cuda")
-    dst_ids = torch.tensor(target, device="cuda")
-    exact = all(torch.equal(t[:, src_ids].view(torch.int16), t[:, dst_ids].view(torch.int16))
-                if t.ndim == 5 else torch.equal(t[src_ids].view(torch.int16), t[dst_ids].view(torch.int16))
-                for t in caches.values())
-    import numpy as np
+    # Parity of the last step, outside the timed region.
     import oracle
-    crcs, shas = oracle.digest_records(staged.pointer, size, size, SESSION_BLOCKS, threads=min(16, os.cpu_count()))
-    digests_exact = all(crc == int(c) and sha == bytes(s).hex()
-                        for (sha, crc), c, s in zip(digests, crcs, shas))
+    exact = same_blocks(torch, caches, source, target)
+    crcs, shas = oracle.digest_records(staged.pointer, size, size, session, threads=min(16, os.cpu_count() or 1))
+    digests_exact = all(crc == int(c) and sha == bytes(s).hex() for (sha, crc), c, s in zip(digests, crcs, shas))
     log(f"parity: restore byte-exact={exact}, CRC32C+SHA-256 bit-exact={digests_exact}")
 
-    gather = kernels["gather"]
-    restore = kernels["restore"]
-    crc = kernels["crc32c"]
-    sha = kernels["sha256"]
-    gather_achieved = 2 * total / (gather["avg_ms"] * 1e6)        # read + write per launch (one launch per save)
-    restore_per_launch = total / restore["launches"] * args.steps   # bytes per launch (pinned read = HBM write)
-    restore_link = restore_per_launch / (restore["avg_ms"] * 1e6)
+    gather, restore, crc, sha = kernels["gather"], kernels["restore"], kernels["crc32c"], kernels["sha256"]
+    gather_achieved = 2 * total / (gather["avg_ms"] * 1e6)          # read + write, one launch per save
+    restore_link = (total * args.steps / restore["launches"]) / (restore["avg_ms"] * 1e6)
     crc_achieved = total / (crc["avg_ms"] * 1e6)
-    cpu = None if args.no_cpu_baseline else cpu_baseline(args.cpu_seconds)
+    cpu = None if args.no_cpu_baseline else cpu_baseline(layers, 65536, args.cpu_seconds)
     out = {
         "metric": "8k Qwen3-8B KV restore/save GB/s and ms; % of host-link and HBM roofline",
         "value": round(2 * total / (ms_per_step * 1e6), 3),
@@ -216,16 +230,18 @@ def main():
         "vs_baseline": None,
         "dtype": "u8",
         "data": "synthetic (seeded bf16 ~N(0,1) KV, seeded block tables)",
-        "config": {"workload": "qwen3-8b-8k-token-snapshot-save-then-restore", "layers": LAYERS,
-                   "kv_heads": HEADS, "head_dim": HEAD_DIM, "block_size": BLOCK_SIZE, "cache_blocks": NUM_BLOCKS,
-                   "session_blocks": SESSION_BLOCKS, "snapshot_bytes": total, "kv_dtype": "bf16",
-                   "layout": args.layout, "parallelism": "none (one GPU)"},
+        "config": {"workload": "qwen3-8b-8k-token-snapshot-save-then-restore", "layers": layers, "kv_heads": 8,
+                   "head_dim": 128, "block_size": block_size, "cache_blocks": num_blocks, "session_blocks": session,
+                   "snapshot_bytes": total, "kv_dtype": "bf16", "layout": args.layout,
+                   "parallelism": "none (one GPU)"},
         "save_ms": round(statistics.median(save_ms), 3),
         "save_gbps": round(total / statistics.median(save_ms) / 1e6, 2),
         "save_hashed_ms": round(statistics.median(hashed_ms), 3),
         "restore_ms": round(statistics.median(restore_ms), 3),
         "restore_gbps": round(total / statistics.median(restore_ms) / 1e6, 2),
         "restore_launches": launches,
+        "restore_early_ready_ms": round(early_ms, 3),
+        "restore_kernels_span_ms": round(restore_span_ms, 3),
         "h2d_peak_gbps": round(h2d_peak, 2),
         "d2h_peak_gbps": round(d2h_peak, 2),
         "restore_frac_of_h2d": round(total / statistics.median(restore_ms) / 1e6 / h2d_peak, 4),
@@ -233,19 +249,285 @@ def main():
         "kernels_ms": {name: round(k["avg_ms"], 4) for name, k in kernels.items()},
         "roofline": {"kernel": "gather_kernel", "bound": "hbm", "achieved": round(gather_achieved, 1),
                      "peak": HBM_PEAK_GBPS, "unit": "GB/s", "frac": round(gather_achieved / HBM_PEAK_GBPS, 4),
-                     "traffic": None},
+                     "traffic": measured_traffic("gather_kernel"), "algorithmic_bytes": 2 * total,
+                     "traffic_source": "profiles/qwen3-8b-8k-kernels.traffic.md (rocprofv3 FETCH_SIZE, WRITE_SIZE)"},
         "link_roofline": {"kernel": "restore_kernel", "bound": "host-link", "achieved": round(restore_link, 2),
                           "peak": round(h2d_peak, 2), "unit": "GB/s", "frac": round(restore_link / h2d_peak, 4)},
         "crc_roofline": {"kernel": "crc_stripes_kernel", "bound": "hbm", "achieved": round(crc_achieved, 1),
                          "peak": HBM_PEAK_GBPS, "unit": "GB/s", "frac": round(crc_achieved / HBM_PEAK_GBPS, 4)},
-        "sha256": {"ms": round(sha["avg_ms"], 3), "gbps": round(total / (sha["avg_ms"] * 1e6), 2),
-                   "records": SESSION_BLOCKS},
+        "sha256": {"kernel": "sha256_kernel", "ms": round(sha["avg_ms"], 3),
+                   "gbps": round(total / (sha["avg_ms"] * 1e6), 2), "records": session},
         "parity": {"restore_byte_exact": exact, "digests_bit_exact": digests_exact},
         "cpu_baseline": cpu,
     }
     staged.close()
     plane.close()
-    print(json.dumps(out), flush=True)
+    return out
+
+
+# ---------------------------------------------------------------- disk-staged restore with fork dedup
+
+def run_disk_fork(args):
+    import torch
+    from kvsnap_amd import synth
+    from kvsnap_amd.blobs import BlobDirectory
+    from kvsnap_amd.dataplane import TorchBlockDataPlane
+    from kvsnap_amd.native_io import IO_LIBRARY, NativeIO
+
+    layers, num_blocks, block_size, tokens, shared = 36, 16384, 16, 32768, 1536
+    n = tokens // block_size
+    caches, backing = synth.make_caches(layers, num_blocks, block_size=block_size, layout=args.layout)
+    size = layers * 65536
+    plane = TorchBlockDataPlane(caches, block_size, 2 * n * size + (64 << 20))
+    plane.warm_up()
+    keep = synth.fill(plane, 0)
+    torch.cuda.synchronize()
+    del keep
+    parent = random.Random(1).sample(range(1, num_blocks), n)
+    taken = set(parent)
+    fresh = random.Random(3).sample([b for b in range(1, num_blocks) if b not in taken], n - shared)
+    child = parent[:shared] + fresh
+    taken |= set(fresh)
+    target = random.Random(2).sample([b for b in range(1, num_blocks) if b not in taken], n)
+    io = NativeIO(IO_LIBRARY, workers=8, queue_bytes=64 << 20)
+    root = tempfile.mkdtemp(prefix="kvsnap-blobs-", dir=args.disk_dir)
+    store = BlobDirectory(root)
+    store.io = io
+    phases, written, segments = {}, {}, {}
+    for name, ids in (("parent", parent), ("child", child)):
+        staged = plane.pool.reserve(n * size)
+        targets = [(staged, i * size) for i in range(n)]
+        digests = []
+        t0 = time.perf_counter()
+        plane.save_gather(ids, targets, tokens, digests=digests)
+        t1 = time.perf_counter()
+        dig = digests[0].result()
+        t2 = time.perf_counter()
+        segments[name] = store.write_blocks([(staged.pointer + i * size, size) for i in range(n)], dig)
+        t3 = time.perf_counter()
+        written[name] = store.written
+        phases[name] = {"gather_d2h_ms": round((t1 - t0) * 1e3, 2), "hashes_ready_ms": round((t2 - t0) * 1e3, 2),
+                        "blob_write_ms": round((t3 - t2) * 1e3, 2)}
+        staged.close()
+    shared_ids = sum(1 for a, b in zip(segments["parent"], segments["child"]) if a["blob_id"] == b["blob_id"])
+    blobs = len(os.listdir(os.path.join(root, "blobs")))
+    log(f"disk-fork: {blobs} blobs, child shares {shared_ids} with parent, wrote {written}")
+    crcs = [s["crc32c"] for s in segments["child"]]
+    restores = {}
+    for verify in ("host", "gpu"):
+        staging = plane.pool.reserve(n * size)
+        sources = [(staging, i * size) for i in range(n)]
+        t0 = time.perf_counter()
+        store.read_prepared_into(segments["child"], staging.pointer, size, workers=8,
+                                 verify="host" if verify == "host" else "none")
+        t1 = time.perf_counter()
+        if verify == "gpu":
+            plane.load_scatter_verified(target, sources, crcs)
+        else:
+            plane.load_scatter(target, sources)
+        t2 = time.perf_counter()
+        exact = same_blocks(torch, caches, child, target)
+        restores[verify] = {"read_ms": round((t1 - t0) * 1e3, 2), "read_gbps": round(n * size / (t1 - t0) / 1e9, 2),
+                            "h2d_scatter_ms": round((t2 - t1) * 1e3, 2),
+                            "h2d_gbps": round(n * size / (t2 - t1) / 1e9, 2),
+                            "total_ms": round((t2 - t0) * 1e3, 2), "byte_exact": exact}
+        staging.close()
+        for t in caches.values():            # scrub the targets between the two restores
+            if t.ndim == 5:
+                t[:, torch.tensor(target, device="cuda")] = 0
+            else:
+                t[torch.tensor(target, device="cuda")] = 0
+    io.close()
+    import shutil
+    shutil.rmtree(root, ignore_errors=True)
+    plane.close()
+    best = min(restores.values(), key=lambda r: r["total_ms"])
+    return {"metric": "disk-staged restore with fork dedup, 32k-token Qwen3-8B", "workload": "disk-fork",
+            "value": round(n * size / best["total_ms"] / 1e6, 3), "unit": "GB/s", "snapshot_bytes": n * size,
+            "blobs_on_disk": blobs, "child_blocks_shared_with_parent": shared_ids, "blobs_written": written,
+            "saves": phases, "restores": restores, "page_cache": "warm (files just written)",
+            "layout": args.layout}
+
+
+# ---------------------------------------------------------------- rotating fp8 sessions under decode load
+
+def run_rotating(args):
+    import torch
+    from kvsnap_amd import synth
+    from kvsnap_amd.dataplane import TorchBlockDataPlane, _check, kernel_library
+
+    layers, num_blocks, block_size = 28, 16384, 16
+    caches, backing = synth.make_caches(layers, num_blocks, block_size=block_size, layout="kv_split",
+                                        dtype=torch.float8_e4m3fn)
+    sessions_tokens = [1024, 2048, 4096, 8192]
+    size = layers * 32768
+    plane = TorchBlockDataPlane(caches, block_size, sum(t // block_size for t in sessions_tokens) * size + (64 << 20))
+    plane.warm_up()
+    scales_rng = random.Random(4)
+    layer_inv = [scales_rng.uniform(0.5, 2.0) for _ in range(layers)]
+    keep = synth.fill(plane, 0, kind=synth.KIND_E4M3, inv_scales=[layer_inv[s // 2] for s in range(2 * layers)])
+    torch.cuda.synchronize()
+    del keep
+    rng = random.Random(1)
+    free = list(range(1, num_blocks))
+    rng.shuffle(free)
+    sessions = []
+    for t in sessions_tokens:
+        count = t // block_size
+        src, dst = free[:count], free[count:2 * count]
+        del free[:2 * count]
+        staged = plane.pool.reserve(count * size)
+        sessions.append((t, src, dst, staged, [(staged, i * size) for i in range(count)]))
+    # decode stand-in: 16 sequences x 4096 tokens (256 blocks) of random paged blocks, every layer's K and V
+    lib = kernel_library()
+    spans = plane.spans()
+    bases = torch.tensor([s[1] for s in spans], dtype=torch.int64, device="cuda")
+    pitches = torch.tensor([s[2] for s in spans], dtype=torch.int64, device="cuda")
+    words = torch.tensor([s[3] // 8 for s in spans], dtype=torch.int64, device="cuda")
+    seqs, per_seq = 16, 256
+    table = torch.tensor([random.Random(100 + q).sample(range(1, num_blocks), per_seq) for q in range(seqs)],
+                         dtype=torch.int64, device="cuda")
+    out = torch.zeros(seqs * len(spans), dtype=torch.int32, device="cuda")
+    compute = torch.cuda.current_stream()
+
+    def decode_step():
+        _check(lib, lib.kvsnap_synth_decode(bases.data_ptr(), pitches.data_ptr(), words.data_ptr(), len(spans),
+                                            table.data_ptr(), seqs, per_seq, out.data_ptr(), 0, compute.cuda_stream))
+
+    def run_steps(count=None, until=None, depth=32):
+        pairs = []
+        i = 0
+        while (count is not None and i < count) or (until is not None and until()):
+            if len(pairs) >= depth:
+                pairs[-depth][1].synchronize()
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record(compute)
+            decode_step()
+            b.record(compute)
+            pairs.append((a, b))
+            i += 1
+        torch.cuda.synchronize()
+        return [a.elapsed_time(b) for a, b in pairs]
+
+    run_steps(50)
+    baseline = run_steps(400)
+    base_med, base_p99 = statistics.median(baseline), percentile(baseline, 99)
+    moved = [0]
+
+    def rotate(rounds):
+        for _ in range(rounds):
+            for tokens, src, dst, staged, targets in sessions:
+                plane.save_gather(src, targets, tokens)
+                plane.load_scatter(dst, targets)
+                moved[0] += 2 * len(src) * size
+
+    t0 = time.perf_counter()
+    rotate(1)                                           # copies alone
+    alone_gbps = moved[0] / (time.perf_counter() - t0) / 1e9
+    moved[0] = 0
+    worker = threading.Thread(target=rotate, args=(args.rounds,))
+    t0 = time.perf_counter()
+    worker.start()
+    loaded = run_steps(until=worker.is_alive)
+    worker.join()
+    elapsed = time.perf_counter() - t0
+    exact = all(same_blocks(torch, caches, src, dst) for _, src, dst, _, _ in sessions)
+    stalls = [max(0.0, t - base_med) for t in loaded]
+    for *_, staged, _ in sessions:
+        staged.close()
+    plane.close()
+    step_bytes = seqs * per_seq * len(spans) * (size // len(spans))
+    return {"metric": "rotating fp8 sessions under decode load, Qwen3-1.7B", "workload": "rotating-fp8",
+            "value": round(moved[0] / elapsed / 1e9, 3), "unit": "GB/s (copy, beside decode)",
+            "copy_alone_gbps": round(alone_gbps, 3), "rounds": args.rounds,
+            "record_bytes": size, "sessions_tokens": sessions_tokens,
+            "decode_step_ms": {"baseline_median": round(base_med, 4), "baseline_p99": round(base_p99, 4),
+                               "loaded_median": round(statistics.median(loaded), 4),
+                               "loaded_p99": round(percentile(loaded, 99), 4), "steps": len(loaded)},
+            "decode_hbm_gbps_baseline": round(step_bytes / base_med / 1e6, 1),
+            "p99_compute_stall_ms": round(percentile(stalls, 99), 4),
+            "restore_programs": plane.restore_programs, "byte_exact": exact}
+
+
+# ---------------------------------------------------------------- kernels alone (profiling driver)
+
+def run_kernels(args):
+    """Each kernel of the default workload alone, HIP-event timed on its stream, plus a plain
+    device-to-device copy of the same byte count (the reference point for rocprof's traffic counters)."""
+    import torch
+    from kvsnap_amd import synth
+    from kvsnap_amd.dataplane import (_check, copy_host_blocks, digest_device_records, gather_blocks,
+                                      kernel_library, TorchBlockDataPlane)
+
+    layers, num_blocks, block_size, tokens = 36, 16384, 16, 8192
+    session = tokens // block_size
+    caches, backing = synth.make_caches(layers, num_blocks, block_size=block_size, layout=args.layout)
+    plane = TorchBlockDataPlane(caches, block_size, session * layers * 65536 + (64 << 20))
+    plane.warm_up()
+    keep = synth.fill(plane, 0)
+    torch.cuda.synchronize()
+    del keep
+    size = plane.block_bytes
+    total = session * size
+    source, target = synth.block_tables(num_blocks, session)
+    tables = plane._load_tables()
+    stream = torch.cuda.current_stream()
+    ids = torch.tensor(source, dtype=torch.int64, device="cuda")
+    stage = torch.empty(total, dtype=torch.uint8, device="cuda")
+    other = torch.empty(total, dtype=torch.uint8, device="cuda")
+    staged = plane.pool.reserve(total)
+    pinned = torch.tensor([staged.pointer + i * size for i in range(session)], dtype=torch.int64, device="cuda")
+    dst = torch.tensor(target, dtype=torch.int64, device="cuda")
+    lib = kernel_library()
+    crc = torch.empty(session, dtype=torch.int32, device="cuda")
+    work_bytes = int(lib.kvsnap_crc32c_workspace_bytes(size, session))
+    work = torch.empty(work_bytes, dtype=torch.uint8, device="cuda")
+    sha = torch.empty((session, 32), dtype=torch.uint8, device="cuda")
+    runs = {
+        "plain_copy": (lambda: other.copy_(stage), 2 * total, args.reps),
+        "gather_kernel": (lambda: gather_blocks(ids, *tables, stage.data_ptr(), size), 2 * total, args.reps),
+        "crc_stripes_kernel": (lambda: _check(lib, lib.kvsnap_crc32c_records(
+            stage.data_ptr(), size, size, session, 0, crc.data_ptr(), work.data_ptr(), work_bytes,
+            stream.cuda_stream)), total, args.reps),
+        "restore_kernel": (lambda: copy_host_blocks(pinned, dst, *tables), 2 * total, args.reps),
+        "sha256_kernel": (lambda: _check(lib, lib.kvsnap_sha256_records(
+            stage.data_ptr(), size, size, session, sha.data_ptr(), stream.cuda_stream)), total, 1),
+    }
+    out = {}
+    for name, (fn, algorithmic, reps) in runs.items():
+        fn()
+        ms = median_ms(torch, stream, fn, reps=reps)
+        out[name] = {"ms": round(ms, 4), "algorithmic_bytes": algorithmic,
+                     "gbps": round(algorithmic / ms / 1e6, 1)}
+    staged.close()
+    plane.close()
+    return {"workload": "kernels", "snapshot_bytes": total, "layout": args.layout, "kernels": out,
+            "note": "restore_kernel reads pinned host records (link) and writes HBM; bytes counted both ways"}
+
+
+def main():
+    parser = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    parser.add_argument("--gpus", type=int, default=1)
+    parser.add_argument("--steps", type=int, default=10)
+    parser.add_argument("--warmup", type=int, default=3)
+    parser.add_argument("--layout", choices=("kv_split", "vllm"), default="kv_split")
+    parser.add_argument("--workload", choices=("save-restore", "disk-fork", "rotating-fp8", "kernels"),
+                        default="save-restore")
+    parser.add_argument("--reps", type=int, default=5, help="kernels: timed repetitions per kernel")
+    parser.add_argument("--rounds", type=int, default=4, help="rotating-fp8: rounds over the four sessions")
+    parser.add_argument("--disk-dir", default=None, help="disk-fork: where the blob files go")
+    parser.add_argument("--cpu-seconds", type=float, default=20.0)
+    parser.add_argument("--no-cpu-baseline", action="store_true")
+    args = parser.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU: every GPU saves and restores its own KV shard over its own host link, "
+              "so there is no multi-GPU step to time here (run with --gpus 1)", file=sys.stderr)
+        sys.exit(2)
+    import torch
+    torch.cuda.set_device(0)
+    runner = {"save-restore": run_save_restore, "disk-fork": run_disk_fork, "rotating-fp8": run_rotating,
+              "kernels": run_kernels}
+    print(json.dumps(runner[args.workload](args)), flush=True)
 
 
 if __name__ == "__main__":

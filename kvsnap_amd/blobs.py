@@ -63,19 +63,27 @@ class BlobDirectory:
         return self.blob_dir / (blob_id + ".blob")
 
     def write_blob(self, blob_id, data, crc32c, *, durable=False):
-        """Write one blob unless a file of that name already exists (content-addressed dedup)."""
+        """Write one blob unless a file of that name already exists (content-addressed dedup).
+
+        ``data`` is bytes-like, or ``(address, size)`` of memory written in
+        place (pinned records).  Returns whether a file was written.
+        """
         final = self.path(blob_id)
+        size = data[1] if isinstance(data, tuple) else len(data)
         if final.exists():
             with final.open("rb") as stream:
                 length, checksum = parse_header(stream.read(HEADER.size))
-            if length != len(data) or checksum != crc32c:
+            if length != size or checksum != crc32c:
                 raise CorruptSnapshotError("existing blob differs from its content id")
             return False
         temporary = self.blob_dir / f"{blob_id}.{uuid.uuid4().hex}.tmp"
         fd = os.open(temporary, os.O_CREAT | os.O_EXCL | os.O_WRONLY, 0o600)
         try:
-            self.io.pwrite_all(fd, pack_header(len(data), crc32c), 0)
-            self.io.pwrite_all(fd, data, HEADER.size)
+            self.io.pwrite_all(fd, pack_header(size, crc32c), 0)
+            if isinstance(data, tuple):
+                self.io.pwrite_at(fd, data[0], size, HEADER.size)
+            else:
+                self.io.pwrite_all(fd, data, HEADER.size)
             if durable:
                 os.fdatasync(fd)
         finally:
@@ -84,22 +92,30 @@ class BlobDirectory:
         return True
 
     def write_blocks(self, blocks, digests, *, durable=False, workers=8):
-        """Write each block under its (sha256 hex, crc32c); returns the segments, one per block."""
+        """Write each block under its (sha256 hex, crc32c); returns the segments, one per block.
+
+        A block whose id repeats, in this call or an earlier one, is written
+        once (reference dedup, kvsnap/connector/volatile.py:261-270,
+        kvsnap/store/store.py:623-627).  ``self.written`` counts the files
+        this call created.
+        """
         if len(blocks) != len(digests):
             raise ValueError("one digest per block is required")
         unique = {}
         for data, (blob_id, crc) in zip(blocks, digests):
             unique.setdefault(blob_id, (data, crc))
         with ThreadPoolExecutor(max_workers=workers, thread_name_prefix="kvsnap-write") as pool:
-            list(pool.map(lambda item: self.write_blob(item[0], item[1][0], item[1][1], durable=durable),
-                          unique.items()))
+            written = list(pool.map(lambda item: self.write_blob(item[0], item[1][0], item[1][1], durable=durable),
+                                    unique.items()))
+        self.written = sum(written)
         if durable:
             fd = os.open(self.blob_dir, os.O_RDONLY | os.O_DIRECTORY)
             try:
                 os.fsync(fd)
             finally:
                 os.close(fd)
-        return [dict(blob_id=blob_id, offset=0, length=len(data), first_block=index, nblocks=1, crc32c=crc)
+        return [dict(blob_id=blob_id, offset=0, length=data[1] if isinstance(data, tuple) else len(data),
+                     first_block=index, nblocks=1, crc32c=crc)
                 for index, (data, (blob_id, crc)) in enumerate(zip(blocks, digests))]
 
     def read_prepared_into(self, segments, address, block_bytes, *, first_block=0, workers=8, verify="host"):

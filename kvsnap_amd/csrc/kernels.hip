@@ -109,6 +109,22 @@ __global__ __launch_bounds__(kGatherThreads) void gather_kernel(
     }
 }
 
+// Gather into per-block destinations (pinned host records written in place
+// over the host link, or anywhere else): the restore kernel's inverse, with
+// its small-grid shape.
+__global__ __launch_bounds__(kRestoreThreads) void gather_to_kernel(
+    const int64_t* __restrict__ dests, const int64_t* __restrict__ blocks, int64_t n_blocks,
+    const int64_t* __restrict__ offs, const int64_t* __restrict__ bases, const int64_t* __restrict__ pitches,
+    const int64_t* __restrict__ words, int64_t n_spans) {
+    const int64_t jobs = n_blocks * n_spans;
+    for (int64_t job = blockIdx.x; job < jobs; job += gridDim.x) {
+        const int64_t b = job / n_spans, s = job - b * n_spans;
+        const char* src = reinterpret_cast<const char*>(bases[s] + blocks[b] * pitches[s]);
+        char* dst = reinterpret_cast<char*>(dests[b] + offs[s]);
+        copy_span<kRestoreThreads, kRestoreUnroll>(src, dst, words[s] * 8);
+    }
+}
+
 // One workgroup per region; regions are small (one token's C elements).
 __global__ __launch_bounds__(kThreads) void zero_kernel(char* __restrict__ base, const int64_t* __restrict__ offsets,
                                                        const int64_t* __restrict__ lengths, int64_t n) {
@@ -207,6 +223,36 @@ __global__ __launch_bounds__(kThreads) void synth_kernel(uint64_t seed, int kind
             }
             dst[v] = u32x4{w[0], w[1], w[2], w[3]};
         }
+    }
+}
+
+// A stand-in for decode attention's KV traffic: every (sequence, span) job
+// streams the span of each block in the sequence's block table (16-byte
+// loads) and folds it into a 32-bit sum, one word per job.
+__global__ __launch_bounds__(kThreads) void synth_decode_kernel(const int64_t* __restrict__ bases,
+                                                               const int64_t* __restrict__ pitches,
+                                                               const int64_t* __restrict__ words, int64_t n_spans,
+                                                               const int64_t* __restrict__ table, int64_t n_seqs,
+                                                               int64_t blocks_per_seq, uint32_t* __restrict__ out) {
+    __shared__ uint32_t red[kThreads / 64];
+    const int64_t jobs = n_seqs * n_spans;
+    for (int64_t job = blockIdx.x; job < jobs; job += gridDim.x) {
+        const int64_t q = job / n_spans, s = job - q * n_spans;
+        const int64_t nv = words[s] / 2;
+        uint32_t acc = 0;
+        for (int64_t k = 0; k < blocks_per_seq; ++k) {
+            const u32x4* src = reinterpret_cast<const u32x4*>(bases[s] + table[q * blocks_per_seq + k] * pitches[s]);
+            for (int64_t v = threadIdx.x; v < nv; v += kThreads) {
+                const u32x4 x = src[v];
+                acc += x.x ^ x.y ^ x.z ^ x.w;
+            }
+        }
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) acc += __shfl_xor(acc, o);
+        if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = acc;
+        __syncthreads();
+        if (threadIdx.x == 0) out[job] = red[0] + red[1] + red[2] + red[3];
+        __syncthreads();
     }
 }
 
@@ -595,6 +641,36 @@ int kvsnap_gather_blocks(const int64_t* blocks, int64_t n_blocks, const int64_t*
                            reinterpret_cast<hipStream_t>(stream), blocks, n_blocks, span_offsets, span_bases,
                            span_pitches, span_words, n_spans, static_cast<char*>(records), record_pitch);
         check_launch("gather");
+    });
+}
+
+int kvsnap_gather_to_records(const int64_t* dests, const int64_t* blocks, int64_t n_blocks,
+                             const int64_t* span_offsets, const int64_t* span_bases, const int64_t* span_pitches,
+                             const int64_t* span_words, int64_t n_spans, int programs, uintptr_t stream) {
+    return guard([&] {
+        if (n_blocks < 0 || n_spans < 0) throw std::runtime_error("negative gather size");
+        if (n_blocks == 0 || n_spans == 0) return;
+        if (!dests || !blocks || !span_offsets || !span_bases || !span_pitches || !span_words)
+            throw std::runtime_error("gather tables must be device pointers");
+        hipLaunchKernelGGL(gather_to_kernel, dim3(grid_for(n_blocks * n_spans, programs)), dim3(kRestoreThreads), 0,
+                           reinterpret_cast<hipStream_t>(stream), dests, blocks, n_blocks, span_offsets, span_bases,
+                           span_pitches, span_words, n_spans);
+        check_launch("gather to records");
+    });
+}
+
+int kvsnap_synth_decode(const int64_t* span_bases, const int64_t* span_pitches, const int64_t* span_words,
+                        int64_t n_spans, const int64_t* block_table, int64_t n_seqs, int64_t blocks_per_seq,
+                        uint32_t* out, int programs, uintptr_t stream) {
+    return guard([&] {
+        if (n_spans < 0 || n_seqs < 0 || blocks_per_seq < 0) throw std::runtime_error("negative decode size");
+        if (n_spans == 0 || n_seqs == 0) return;
+        if (!span_bases || !span_pitches || !span_words || !block_table || !out)
+            throw std::runtime_error("decode tables must be device pointers");
+        hipLaunchKernelGGL(synth_decode_kernel, dim3(grid_for(n_seqs * n_spans, programs)), dim3(kThreads), 0,
+                           reinterpret_cast<hipStream_t>(stream), span_bases, span_pitches, span_words, n_spans,
+                           block_table, n_seqs, blocks_per_seq, out);
+        check_launch("synthetic decode");
     });
 }
 

@@ -83,3 +83,17 @@ def test_a_corrupt_or_missing_blob_is_refused_before_any_copy(tmp_path):
         store.read_prepared_into(segments[:1], C.addressof(target), 4096)
     with pytest.raises(CorruptSnapshotError, match="identifier"):
         store.path("../etc/passwd")
+
+
+def test_blocks_written_from_memory_in_place_and_dedup_counts(tmp_path):
+    store = BlobDirectory(tmp_path, io_backend="native")
+    blocks = records(3, 5000, seed=8)
+    buf = C.create_string_buffer(b"".join(blocks), 15000)
+    parts = [(C.addressof(buf) + i * 5000, 5000) for i in range(3)]
+    segments = store.write_blocks(parts, digests(blocks))
+    assert store.written == 3 and [s["length"] for s in segments] == [5000] * 3
+    for block, segment in zip(blocks, segments):
+        assert (tmp_path / "blobs" / (segment["blob_id"] + ".blob")).read_bytes()[32:] == block
+    child = blocks[:2] + records(1, 5000, seed=9)
+    store.write_blocks(child, digests(child))
+    assert store.written == 1 and len(list((tmp_path / "blobs").glob("*.blob"))) == 4

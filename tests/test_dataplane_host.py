@@ -462,3 +462,30 @@ def test_registration_requires_one_cuda_device():
         cpu.device = SimpleNamespace(type="cpu", index=None)
         with pytest.raises(ValueError, match="one CUDA device"):
             TorchBlockDataPlane({"layer.0": cpu}, 4, 4096)
+
+
+def test_early_report_follows_the_reference_rule():
+    """vllm.py:649-679 as pinned by test_failure_policy.py:180-206."""
+    from kvsnap_amd.ordering import EARLY_REPORT_BYTES, copy_left, early_launch_index, early_report
+    mib = 1 << 20
+    done, pending = Mock(query=Mock(return_value=True)), Mock(query=Mock(return_value=False))
+    progress = [(None, 300 * mib), (done, 200 * mib), (done, 100 * mib), (pending, 0)]
+    assert copy_left(progress) == 100 * mib
+    assert early_report(progress) == (100 * mib, pending)
+    assert early_report([(None, 300 * mib), (done, 200 * mib), (pending, 100 * mib), (pending, 0)]) is None
+    assert copy_left([(None, 300 * mib), (done, 100 * mib), (pending, 50 * mib)]) is None     # still queuing
+    assert EARLY_REPORT_BYTES == 128 * mib
+    assert early_launch_index(progress) == 1
+    # the oracle's restatement of the same rule agrees on the same scenario
+    assert oracle.copy_left([(None if e is None else e.query, l) for e, l in progress]) == copy_left(progress)
+
+
+def test_restore_progress_reaches_the_early_report_threshold_at_the_expected_launch(qwen):
+    """An 8k-token Qwen3-8B restore: 19 launches of 28 blocks; reportable after the 17th."""
+    from kvsnap_amd.ordering import early_launch_index
+    size = 36 * 65536
+    per_launch = (64 << 20) // size
+    progress = [(None, 512 * size)] + [(Mock(), (512 - min(512, (k + 1) * per_launch)) * size)
+                                       for k in range(-(-512 // per_launch))]
+    assert len(progress) - 1 == 19
+    assert early_launch_index(progress) == 16

@@ -255,3 +255,126 @@ def test_restore_from_device_memory_uses_the_same_kernel(planes):
         for layer, name in enumerate(sorted(caches)):
             span = caches[name][block].permute(1, 0, 2).contiguous().view(torch.int16).reshape(-1)
             assert torch.equal(span, records[i][layer * 32768:(layer + 1) * 32768])
+
+
+@pytest.mark.parametrize("layout", ["vllm", "kv_split"])
+def test_direct_save_writes_pinned_records_in_place(hip_library, oracle_lib, layout):
+    caches, backing = synth.make_caches(LAYERS, 24, layout=layout)
+    plane = TorchBlockDataPlane(caches, BLOCK_SIZE, 64 << 20, save_mode="direct")
+    try:
+        plane.warm_up()
+        keep = synth.fill(plane, 13, kind=synth.KIND_BYTES)
+        host = host_copy(backing)
+        del keep
+        block_ids, tokens = [7, 2, 9, 3, 4], 4 * BLOCK_SIZE + 5
+        size = plane.block_bytes
+        records = oracle_lib.gather(host_spans(plane, backing, host), block_ids, size)
+        oracle_lib.zero_tail(records[-1], plane.layers, 5)
+        for kind in ("per-block", "staging"):
+            owned = ([plane.pool.reserve(size * len(block_ids))] if kind == "staging"
+                     else [plane.pool.reserve(size) for _ in block_ids])
+            targets = ([(owned[0], i * size) for i in range(len(block_ids))] if kind == "staging"
+                       else [(allocation, 0) for allocation in owned])
+            digests = []
+            assert plane.save_gather(block_ids, targets, tokens, chunk_bytes=2 * size, digests=digests) == 3
+            for index, (allocation, offset) in enumerate(targets):
+                assert np.array_equal(pinned_bytes(allocation, offset, size), records[index]), (kind, index)
+            for (hexdigest, crc), record in zip(digests[0].result(), records):
+                assert crc == oracle_lib.crc32c(record) and hexdigest == hashlib.sha256(record.tobytes()).hexdigest()
+            for allocation in owned:
+                allocation.close()
+        assert np.array_equal(host_copy(backing), host)
+    finally:
+        torch.cuda.synchronize()
+        plane.close()
+
+
+def test_verified_restore_checks_every_block_before_writing_any(planes, oracle_lib):
+    from kvsnap_amd.blobs import CorruptSnapshotError
+    caches, backing = synth.make_caches(LAYERS, 40, layout="kv_split")
+    plane = planes(caches)
+    keep = synth.fill(plane, 21)
+    torch.cuda.synchronize()
+    del keep
+    saved, restored = synth.block_tables(40, 12)
+    size = plane.block_bytes
+    staged = plane.pool.reserve(12 * size)
+    sources = [(staged, i * size) for i in range(12)]
+    digests = []
+    plane.save_gather(saved, sources, 12 * BLOCK_SIZE, digests=digests)
+    crcs = [crc for _, crc in digests[0].result()]
+    before = host_copy(backing)
+    # one flipped bit in the tenth staged block: nothing may reach the cache
+    C.memmove(staged.pointer + 9 * size + 777, bytes([C.string_at(staged.pointer + 9 * size + 777, 1)[0] ^ 4]), 1)
+    with pytest.raises(CorruptSnapshotError, match="block 9"):
+        plane.load_scatter_verified(restored, sources, crcs)
+    assert np.array_equal(host_copy(backing), before)
+    C.memmove(staged.pointer + 9 * size + 777, bytes([C.string_at(staged.pointer + 9 * size + 777, 1)[0] ^ 4]), 1)
+    progress = []
+    assert plane.load_scatter_verified(restored, sources, crcs, progress=progress, chunk_bytes=5 * size) == 3
+    assert [left for _, left in progress] == [12 * size, 7 * size, 2 * size, 0]
+    expected = before.copy()
+    oracle_lib.scatter(host_spans(plane, backing, expected), restored, [staged.pointer + i * size for i in range(12)])
+    assert np.array_equal(host_copy(backing), expected)
+    staged.close()
+
+
+def test_synthetic_decode_reads_every_block_of_every_sequence(planes):
+    caches, backing = synth.make_caches(4, 64, layout="kv_split", dtype=torch.float8_e4m3fn)
+    plane = planes(caches)
+    keep = synth.fill(plane, 5, kind=synth.KIND_BYTES)
+    torch.cuda.synchronize()
+    del keep
+    lib = kernel_library()
+    spans = plane.spans()
+    bases = torch.tensor([s[1] for s in spans], dtype=torch.int64, device="cuda")
+    pitches = torch.tensor([s[2] for s in spans], dtype=torch.int64, device="cuda")
+    words = torch.tensor([s[3] // 8 for s in spans], dtype=torch.int64, device="cuda")
+    table = torch.tensor([random.Random(q).sample(range(64), 9) for q in range(3)], dtype=torch.int64, device="cuda")
+    out = torch.zeros(3 * len(spans), dtype=torch.int32, device="cuda")
+    _check(lib, lib.kvsnap_synth_decode(bases.data_ptr(), pitches.data_ptr(), words.data_ptr(), len(spans),
+                                        table.data_ptr(), 3, 9, out.data_ptr(), 0,
+                                        torch.cuda.current_stream().cuda_stream))
+    torch.cuda.synchronize()
+    host = host_copy(backing)
+    base = backing.data_ptr()
+    for q in range(3):
+        for s, (_, b0, pitch, nbytes) in enumerate(spans):
+            total = 0
+            for block in table[q].tolist():
+                start = b0 - base + block * pitch
+                w = host[start:start + nbytes].view(np.uint32).reshape(-1, 4).astype(np.uint64)
+                total += int((w[:, 0].astype(np.uint32) ^ w[:, 1].astype(np.uint32) ^ w[:, 2].astype(np.uint32)
+                              ^ w[:, 3].astype(np.uint32)).astype(np.uint64).sum())
+            assert (int(out[q * len(spans) + s]) & 0xFFFFFFFF) == total & 0xFFFFFFFF
+
+
+def test_qwen3_1_7b_round_trip_at_the_cpu_reference_shape(planes, oracle_lib):
+    """28 layers, 4096-block cache, a 2048-token (128-block) session: gather, CRC32C, scatter, compare."""
+    caches, backing = synth.make_caches(28, 4096, layout="vllm")
+    plane = planes(caches, capacity=256 << 20)
+    keep = synth.fill(plane, 0)
+    torch.cuda.synchronize()
+    del keep
+    assert plane.block_bytes == 1835008
+    saved, restored = synth.block_tables(4096, 128)
+    size = plane.block_bytes
+    staged = plane.pool.reserve(128 * size)
+    targets = [(staged, i * size) for i in range(128)]
+    digests = []
+    plane.save_gather(saved, targets, 2048, digests=digests)
+    # records against the oracle's generator (no device copy involved) and its CRC
+    for index in (0, 57, 127):
+        record = pinned_bytes(staged, index * size, size)
+        for s, (offset, _, _, nbytes) in enumerate(plane.spans()):
+            assert np.array_equal(record[offset:offset + nbytes],
+                                  oracle_lib.fill_span(0, s, saved[index], nbytes, synth.KIND_BF16)), (index, s)
+    crcs, _ = oracle_lib.digest_records(staged.pointer, size, size, 128, sha=False, threads=8)
+    assert [crc for _, crc in digests[0].result()] == crcs.tolist()
+    plane.load_scatter(restored, targets)
+    torch.cuda.synchronize()
+    src = torch.tensor(saved, device="cuda")
+    dst = torch.tensor(restored, device="cuda")
+    for view in caches.values():
+        assert torch.equal(view[src].view(torch.int16), view[dst].view(torch.int16))
+    staged.close()
