@@ -11,7 +11,10 @@ seeded block table with the restore kernel.  1,207,959,552 bytes each way.
     python bench.py [--steps K] [--warmup W] [--layout kv_split|vllm]
 
 prints one JSON line: ``value`` = (save bytes + restore bytes) / time per
-step, with the cache resident in HBM; plus save/restore latency and GB/s, the
+step, with the cache resident in HBM.  In the timed steps a save's digests are
+collected ``--hash-depth`` (2) steps later, so the hashes of consecutive saves
+run side by side on their own streams; every digest is complete before the
+timer stops.  Also reported: one-at-a-time save/restore latency and GB/s, the
 measured pinned<->device DMA peaks and the fractions of them reached,
 early-readiness latency, per-kernel HIP-event durations, the rooflines, and
 the CPU path timed on this host's cores.
@@ -166,44 +169,67 @@ def run_save_restore(args):
     h2d_peak, d2h_peak = link_peaks(torch, staged, plane._copy_stream, total)
     log(f"DMA peaks: H2D {h2d_peak:.1f} GB/s, D2H {d2h_peak:.1f} GB/s")
 
-    save_ms, hashed_ms, restore_ms = [], [], []
-
-    def step(record):
+    # Latency, one operation at a time (not the timed region): save until the
+    # D2H fence, save until its CRC32C and SHA-256 are ready, restore, and the
+    # restore's early-readiness point.
+    latency = {"save": [], "hashed": [], "restore": [], "early": []}
+    lat_timer = KernelTimer()
+    for i in range(3):
+        plane.timer = lat_timer if i else None
         digests, progress = [], []
         t0 = time.perf_counter()
         plane.save_gather(source, targets, tokens, digests=digests)
         t1 = time.perf_counter()
-        plane.load_scatter(target, targets, progress=progress)
+        digests[0].result()
         t2 = time.perf_counter()
-        result = digests[0].result()
+        plane.load_scatter(target, targets, progress=progress)
         t3 = time.perf_counter()
-        if record:
-            save_ms.append((t1 - t0) * 1e3)
-            restore_ms.append((t2 - t1) * 1e3)
-            hashed_ms.append((t3 - t0) * 1e3)
-        return result, progress
+        if i:
+            latency["save"].append((t1 - t0) * 1e3)
+            latency["hashed"].append((t2 - t0) * 1e3)
+            latency["restore"].append((t3 - t2) * 1e3)
+            launches = len(progress) - 1
+            pairs = lat_timer.pairs["restore"][-launches:]
+            latency["early"].append(pairs[0][0].elapsed_time(pairs[early_launch_index(progress)][1]))
+    plane.timer = None
+    lat = {k: statistics.median(v) for k, v in latency.items()}
+
+    # Throughput: each step saves the session (gather, D2H, GPU CRC32C +
+    # SHA-256) and restores it into the target blocks.  A save's digests are
+    # collected ``hash_depth`` steps later, as a connector's commit thread
+    # would; the timed region ends only when every digest is complete.
+    from collections import deque
+    pending, collected = deque(), []
+
+    def step():
+        digests = []
+        plane.save_gather(source, targets, tokens, digests=digests)
+        plane.load_scatter(target, targets)
+        pending.append(digests[0])
+        while len(pending) > args.hash_depth:
+            collected[:] = [pending.popleft().result()]
+
+    def drain():
+        while pending:
+            collected[:] = [pending.popleft().result()]
+        return collected[0]
 
     for _ in range(args.warmup):
-        step(False)
+        step()
+    drain()
     timer = KernelTimer()
     plane.timer = timer
     torch.cuda.synchronize()
     start = time.perf_counter()
     for _ in range(args.steps):
-        digests, progress = step(True)
+        step()
+    digests = drain()
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - start
     plane.timer = None
     kernels = timer.summary()
     ms_per_step = elapsed * 1e3 / args.steps
-
-    # Early readiness: a load may be reported once every launch is queued and at
-    # most 128 MiB remain; time from the first restore launch to the completion
-    # of the launch after which that holds (last step's events).
-    launches = len(progress) - 1
-    restore_pairs = timer.pairs["restore"][-launches:]
-    early_ms = restore_pairs[0][0].elapsed_time(restore_pairs[early_launch_index(progress)][1])
-    restore_span_ms = restore_pairs[0][0].elapsed_time(restore_pairs[-1][1])
+    launches = kernels["restore"]["launches"] // args.steps
 
     # Parity of the last step, outside the timed region.
     import oracle
@@ -234,18 +260,18 @@ def run_save_restore(args):
                    "head_dim": 128, "block_size": block_size, "cache_blocks": num_blocks, "session_blocks": session,
                    "snapshot_bytes": total, "kv_dtype": "bf16", "layout": args.layout,
                    "parallelism": "none (one GPU)"},
-        "save_ms": round(statistics.median(save_ms), 3),
-        "save_gbps": round(total / statistics.median(save_ms) / 1e6, 2),
-        "save_hashed_ms": round(statistics.median(hashed_ms), 3),
-        "restore_ms": round(statistics.median(restore_ms), 3),
-        "restore_gbps": round(total / statistics.median(restore_ms) / 1e6, 2),
+        "hash_depth": args.hash_depth,
+        "save_ms": round(lat["save"], 3),
+        "save_gbps": round(total / lat["save"] / 1e6, 2),
+        "save_hashed_ms": round(lat["hashed"], 3),
+        "restore_ms": round(lat["restore"], 3),
+        "restore_gbps": round(total / lat["restore"] / 1e6, 2),
         "restore_launches": launches,
-        "restore_early_ready_ms": round(early_ms, 3),
-        "restore_kernels_span_ms": round(restore_span_ms, 3),
+        "restore_early_ready_ms": round(lat["early"], 3),
         "h2d_peak_gbps": round(h2d_peak, 2),
         "d2h_peak_gbps": round(d2h_peak, 2),
-        "restore_frac_of_h2d": round(total / statistics.median(restore_ms) / 1e6 / h2d_peak, 4),
-        "save_frac_of_d2h": round(total / statistics.median(save_ms) / 1e6 / d2h_peak, 4),
+        "restore_frac_of_h2d": round(total / lat["restore"] / 1e6 / h2d_peak, 4),
+        "save_frac_of_d2h": round(total / lat["save"] / 1e6 / d2h_peak, 4),
         "kernels_ms": {name: round(k["avg_ms"], 4) for name, k in kernels.items()},
         "roofline": {"kernel": "gather_kernel", "bound": "hbm", "achieved": round(gather_achieved, 1),
                      "peak": HBM_PEAK_GBPS, "unit": "GB/s", "frac": round(gather_achieved / HBM_PEAK_GBPS, 4),
@@ -514,6 +540,8 @@ def main():
     parser.add_argument("--workload", choices=("save-restore", "disk-fork", "rotating-fp8", "kernels"),
                         default="save-restore")
     parser.add_argument("--reps", type=int, default=5, help="kernels: timed repetitions per kernel")
+    parser.add_argument("--hash-depth", type=int, default=2,
+                        help="save-restore: steps a save's digests may trail before they are collected")
     parser.add_argument("--rounds", type=int, default=4, help="rotating-fp8: rounds over the four sessions")
     parser.add_argument("--disk-dir", default=None, help="disk-fork: where the blob files go")
     parser.add_argument("--cpu-seconds", type=float, default=20.0)

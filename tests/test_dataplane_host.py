@@ -137,10 +137,15 @@ class CudaLabelled:
         return self.tensor[index]
 
 
+def emulated_gather_launcher(*args, **kwargs):
+    return lambda: emulated_gather(*args, **kwargs)
+
+
 @pytest.fixture(autouse=True)
 def emulated_launches():
     with patch.object(dataplane, "copy_host_blocks", emulated_restore), \
          patch.object(dataplane, "gather_blocks", emulated_gather), \
+         patch.object(dataplane, "gather_launcher", emulated_gather_launcher), \
          patch.object(dataplane, "kernel_library", lambda library=None: None), \
          patch.object(TorchBlockDataPlane, "_zero_regions", staticmethod(emulated_zero)):
         yield
