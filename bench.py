@@ -340,25 +340,36 @@ def run_disk_fork(args):
     log(f"disk-fork: {blobs} blobs, child shares {shared_ids} with parent, wrote {written}")
     crcs = [s["crc32c"] for s in segments["child"]]
     restores = {}
-    for verify in ("host", "gpu"):
-        staging = plane.pool.reserve(n * size)
-        sources = [(staging, i * size) for i in range(n)]
+    variants = [("host", "host", False, 8), ("gpu", "gpu", False, 8), ("pipelined-gpu", "gpu", True, 8),
+                ("pipelined-gpu-16", "gpu", True, 16), ("pipelined-host-16", "host", True, 16)]
+    for label, verify, pipelined, workers in variants:
+        io.close()
+        io = NativeIO(IO_LIBRARY, workers=workers, queue_bytes=64 << 20)
+        store.io = io
         t0 = time.perf_counter()
-        store.read_prepared_into(segments["child"], staging.pointer, size, workers=8,
-                                 verify="host" if verify == "host" else "none")
-        t1 = time.perf_counter()
-        if verify == "gpu":
-            plane.load_scatter_verified(target, sources, crcs)
+        if pipelined:
+            plane.load_from_disk(target, store, segments["child"], workers=workers, verify=verify)
+            t1 = t2 = time.perf_counter()
         else:
-            plane.load_scatter(target, sources)
-        t2 = time.perf_counter()
+            staging = plane.pool.reserve(n * size)
+            sources = [(staging, i * size) for i in range(n)]
+            store.read_prepared_into(segments["child"], staging.pointer, size, workers=workers,
+                                     verify="host" if verify == "host" else "none")
+            t1 = time.perf_counter()
+            if verify == "gpu":
+                plane.load_scatter_verified(target, sources, crcs)
+            else:
+                plane.load_scatter(target, sources)
+            t2 = time.perf_counter()
+            staging.close()
         exact = same_blocks(torch, caches, child, target)
-        restores[verify] = {"read_ms": round((t1 - t0) * 1e3, 2), "read_gbps": round(n * size / (t1 - t0) / 1e9, 2),
-                            "h2d_scatter_ms": round((t2 - t1) * 1e3, 2),
-                            "h2d_gbps": round(n * size / (t2 - t1) / 1e9, 2),
-                            "total_ms": round((t2 - t0) * 1e3, 2), "byte_exact": exact}
-        staging.close()
-        for t in caches.values():            # scrub the targets between the two restores
+        entry = {"verify": verify, "read_workers": workers, "total_ms": round((t2 - t0) * 1e3, 2),
+                 "gbps": round(n * size / (t2 - t0) / 1e9, 2), "byte_exact": exact}
+        if not pipelined:
+            entry.update(read_ms=round((t1 - t0) * 1e3, 2), read_gbps=round(n * size / (t1 - t0) / 1e9, 2),
+                         h2d_scatter_ms=round((t2 - t1) * 1e3, 2), h2d_gbps=round(n * size / (t2 - t1) / 1e9, 2))
+        restores[label] = entry
+        for t in caches.values():            # scrub the targets between restores
             if t.ndim == 5:
                 t[:, torch.tensor(target, device="cuda")] = 0
             else:
@@ -367,9 +378,9 @@ def run_disk_fork(args):
     import shutil
     shutil.rmtree(root, ignore_errors=True)
     plane.close()
-    best = min(restores.values(), key=lambda r: r["total_ms"])
     return {"metric": "disk-staged restore with fork dedup, 32k-token Qwen3-8B", "workload": "disk-fork",
-            "value": round(n * size / best["total_ms"] / 1e6, 3), "unit": "GB/s", "snapshot_bytes": n * size,
+            "value": restores["pipelined-gpu"]["gbps"], "unit": "GB/s (pread 8 workers, GPU CRC check, pipelined)",
+            "snapshot_bytes": n * size,
             "blobs_on_disk": blobs, "child_blocks_shared_with_parent": shared_ids, "blobs_written": written,
             "saves": phases, "restores": restores, "page_cache": "warm (files just written)",
             "layout": args.layout}

@@ -378,3 +378,95 @@ def test_qwen3_1_7b_round_trip_at_the_cpu_reference_shape(planes, oracle_lib):
     for view in caches.values():
         assert torch.equal(view[src].view(torch.int16), view[dst].view(torch.int16))
     staged.close()
+
+
+@pytest.mark.parametrize("seed", range(6))
+def test_copy_kernels_on_random_span_tables_including_8_byte_alignment(hip_library, oracle_lib, seed):
+    """Random geometries: odd word counts, pitches that are odd multiples of 8 bytes, bases offset by 8,
+    so the kernels' 8-byte path runs beside the 16-byte one; gather, restore and gather-to-records."""
+    rng = np.random.default_rng(100 + seed)
+    blocks = int(rng.integers(4, 40))
+    n_spans = int(rng.integers(1, 9))
+    words = [int(rng.integers(1, 700)) for _ in range(n_spans)]
+    pitches = [w + int(rng.integers(0, 5)) for w in words]                     # 8-byte words
+    shifts = [int(rng.integers(0, 2)) for _ in range(n_spans)]                 # 0 or 1 word of misalignment
+    offsets = np.cumsum([0] + words[:-1]).tolist()
+    record_words = sum(words)
+    stores = [torch.randint(-2**62, 2**62, (blocks * p + 2,), dtype=torch.int64, device="cuda") for p in pitches]
+    lib = kernel_library()
+    stream = torch.cuda.current_stream().cuda_stream
+
+    def dev(values):
+        return torch.tensor(values, dtype=torch.int64, device="cuda")
+
+    offs = dev([o * 8 for o in offsets])
+    bases = dev([s.data_ptr() + 8 * sh for s, sh in zip(stores, shifts)])
+    pitch_b = dev([p * 8 for p in pitches])
+    words_t = dev(words)
+    count = int(rng.integers(1, blocks + 1))
+    ids = rng.choice(blocks, count, replace=False).tolist()
+    host_before = [s.cpu().numpy().copy() for s in stores]
+    spans = [(h.ctypes.data + 8 * sh, p * 8, o * 8, w * 8)
+             for h, sh, p, o, w in zip(host_before, shifts, pitches, offsets, words)]
+    expected = oracle_lib.gather(spans, ids, record_words * 8)
+    # gather into a device buffer at an 8-byte (not 16) offset
+    out = torch.zeros(count * record_words + 1, dtype=torch.int64, device="cuda")
+    _check(lib, lib.kvsnap_gather_blocks(dev(ids).data_ptr(), count, offs.data_ptr(), bases.data_ptr(),
+                                         pitch_b.data_ptr(), words_t.data_ptr(), n_spans, out.data_ptr() + 8,
+                                         record_words * 8, 0, stream))
+    torch.cuda.synchronize()
+    got = out.cpu().numpy()[1:].view(np.uint8).reshape(count, -1)
+    assert np.array_equal(got, expected)
+    # gather-to-records: per-record destinations
+    dests = torch.zeros(count * (record_words + 1), dtype=torch.int64, device="cuda")
+    dest_ptrs = dev([dests.data_ptr() + 8 * i * (record_words + 1) for i in range(count)])
+    _check(lib, lib.kvsnap_gather_to_records(dest_ptrs.data_ptr(), dev(ids).data_ptr(), count, offs.data_ptr(),
+                                             bases.data_ptr(), pitch_b.data_ptr(), words_t.data_ptr(), n_spans, 7,
+                                             stream))
+    torch.cuda.synchronize()
+    rows = dests.cpu().numpy().reshape(count, record_words + 1)[:, :record_words]
+    assert np.array_equal(rows.view(np.uint8).reshape(count, -1), expected)
+    # restore the gathered records into other blocks
+    targets = rng.choice(blocks, count, replace=False).tolist()
+    sources = dev([out.data_ptr() + 8 + i * record_words * 8 for i in range(count)])
+    _check(lib, lib.kvsnap_restore_blocks(sources.data_ptr(), dev(targets).data_ptr(), count, offs.data_ptr(),
+                                          bases.data_ptr(), pitch_b.data_ptr(), words_t.data_ptr(), n_spans, 5,
+                                          stream))
+    torch.cuda.synchronize()
+    after = [s.cpu().numpy() for s in stores]
+    oracle_lib.scatter(spans, targets, [expected[i].ctypes.data for i in range(count)])
+    for a, h in zip(after, host_before):
+        assert np.array_equal(a, h)
+
+
+@pytest.mark.parametrize("verify", ["gpu", "host"])
+def test_pipelined_disk_restore_is_byte_exact_and_refuses_corrupt_blobs(planes, oracle_lib, tmp_path, verify):
+    from kvsnap_amd.blobs import BlobDirectory, CorruptSnapshotError
+    caches, backing = synth.make_caches(LAYERS, 48, layout="kv_split")
+    plane = planes(caches, capacity=128 << 20)
+    keep = synth.fill(plane, 31)
+    torch.cuda.synchronize()
+    del keep
+    saved, restored = synth.block_tables(48, 20)
+    size = plane.block_bytes
+    staged = plane.pool.reserve(20 * size)
+    digests = []
+    plane.save_gather(saved, [(staged, i * size) for i in range(20)], 20 * BLOCK_SIZE, digests=digests)
+    store = BlobDirectory(tmp_path)
+    segments = store.write_blocks([(staged.pointer + i * size, size) for i in range(20)], digests[0].result())
+    expected = host_copy(backing)
+    oracle_lib.scatter(host_spans(plane, backing, expected), restored, [staged.pointer + i * size for i in range(20)])
+    progress = []
+    launches = plane.load_from_disk(restored, store, segments, chunk_bytes=6 * size, workers=3, verify=verify,
+                                    progress=progress)
+    assert launches == 4 and progress[0] == (None, 20 * size) and progress[-1][1] == 0
+    assert [left for _, left in progress[1:]] == [14 * size, 8 * size, 2 * size, 0]
+    assert np.array_equal(host_copy(backing), expected)
+    # a flipped payload bit in the third chunk's blob
+    path = store.path(segments[13]["blob_id"])
+    raw = bytearray(path.read_bytes())
+    raw[-100] ^= 8
+    path.write_bytes(bytes(raw))
+    with pytest.raises(CorruptSnapshotError):
+        plane.load_from_disk(restored, store, segments, chunk_bytes=6 * size, workers=3, verify=verify)
+    staged.close()
