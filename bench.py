@@ -43,6 +43,25 @@ import threading
 import time
 
 HBM_PEAK_GBPS = 8000.0
+# SHA-256 runs one dependency chain per record (two lanes of a round wave).
+# The round wave issues 648 VALU per 64-byte block (counted in the gfx950 ISA
+# of sha256_kernel: 192 alignbit, 192 bitop3, 127 DPP adds, 65 add3, 64 xad,
+# 8 others); a wave64 VALU takes 4 cycles of its SIMD at the 2.4 GHz peak
+# engine clock.  All chains run side by side (one round wave per 32 records).
+SHA_VALU_PER_BLOCK = 648
+SHA_CYCLES_PER_VALU = 4
+ENGINE_CLOCK_GHZ = 2.4
+
+
+def sha_issue_bound(record_bytes, records, ms):
+    """Fraction of the per-chain VALU issue bound the SHA-256 kernel reached."""
+    blocks = record_bytes // 64 + (1 if record_bytes % 64 + 9 <= 64 else 2)
+    bound_ms = blocks * SHA_VALU_PER_BLOCK * SHA_CYCLES_PER_VALU / (ENGINE_CLOCK_GHZ * 1e6)
+    total = record_bytes * records
+    return {"bound": "valu-issue (one chain per record)", "valu_per_block": SHA_VALU_PER_BLOCK,
+            "cycles_per_valu": SHA_CYCLES_PER_VALU, "clock_ghz": ENGINE_CLOCK_GHZ, "bound_ms": round(bound_ms, 3),
+            "achieved": round(total / (ms * 1e6), 2), "peak": round(total / (bound_ms * 1e6), 2), "unit": "GB/s",
+            "frac": round(bound_ms / ms, 4)}
 
 
 def log(*args):
@@ -282,7 +301,8 @@ def run_save_restore(args):
         "crc_roofline": {"kernel": "crc_stripes_kernel", "bound": "hbm", "achieved": round(crc_achieved, 1),
                          "peak": HBM_PEAK_GBPS, "unit": "GB/s", "frac": round(crc_achieved / HBM_PEAK_GBPS, 4)},
         "sha256": {"kernel": "sha256_kernel", "ms": round(sha["avg_ms"], 3),
-                   "gbps": round(total / (sha["avg_ms"] * 1e6), 2), "records": session},
+                   "gbps": round(total / (sha["avg_ms"] * 1e6), 2), "records": session,
+                   "issue_roofline": sha_issue_bound(size, session, sha["avg_ms"])},
         "parity": {"restore_byte_exact": exact, "digests_bit_exact": digests_exact},
         "cpu_baseline": cpu,
     }
@@ -536,6 +556,7 @@ def run_kernels(args):
         ms = median_ms(torch, stream, fn, reps=reps)
         out[name] = {"ms": round(ms, 4), "algorithmic_bytes": algorithmic,
                      "gbps": round(algorithmic / ms / 1e6, 1)}
+    out["sha256_kernel"]["issue_roofline"] = sha_issue_bound(size, session, out["sha256_kernel"]["ms"])
     staged.close()
     plane.close()
     return {"workload": "kernels", "snapshot_bytes": total, "layout": args.layout, "kernels": out,

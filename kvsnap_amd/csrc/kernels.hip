@@ -390,12 +390,10 @@ __device__ __forceinline__ uint32_t rotr(uint32_t x, int n) { return (x >> n) | 
 __device__ __forceinline__ uint32_t xor3(uint32_t a, uint32_t b, uint32_t c) {
     return __builtin_amdgcn_bitop3_b32(a, b, c, 0x96);
 }
-__device__ __forceinline__ uint32_t maj3(uint32_t a, uint32_t b, uint32_t c) {
-    return __builtin_amdgcn_bitop3_b32(a, b, c, 0xE8);
-}
 __device__ __forceinline__ uint32_t bswap(uint32_t x) { return __builtin_bswap32(x); }
 
 constexpr int kShaBlockQuads = 16;  // 64 schedule words per block, read 4 at a time
+constexpr int kShaColumns = 65;     // 64 records, then {1,1,1,1} for the a-lanes
 
 // Block `blk` of a record as 16 big-endian words, FIPS 180-4 padding included:
 // blocks [0, whole) are payload, then 1 or 2 final blocks carry the tail,
@@ -444,8 +442,32 @@ __device__ __forceinline__ void sha_message(const uint8_t* __restrict__ p, uint6
     }
 }
 
+// Block `blk` as 16 words whose byte swaps are the message words: payload
+// blocks of aligned records are the loaded words themselves, so the swap can
+// wait until the loads have landed.
+template <bool kAligned>
+__device__ __forceinline__ void sha_message_raw(const uint8_t* __restrict__ p, uint64_t record_bytes, uint64_t whole,
+                                                int nfinal, uint64_t blk, uint32_t raw[16]) {
+    if (kAligned && blk < whole) {
+        const u32x4* q = reinterpret_cast<const u32x4*>(p + 64 * blk);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const u32x4 v = q[i];
+            raw[4 * i] = v.x;
+            raw[4 * i + 1] = v.y;
+            raw[4 * i + 2] = v.z;
+            raw[4 * i + 3] = v.w;
+        }
+        return;
+    }
+    uint32_t w[16];
+    sha_message<kAligned>(p, record_bytes, whole, nfinal, blk, w);
+#pragma unroll
+    for (int i = 0; i < 16; ++i) raw[i] = bswap(w[i]);
+}
+
 // Producer: W[t] + K[t] for t = 0..63 into one LDS slot, [quad][lane].
-__device__ __forceinline__ void sha_schedule(uint32_t w[16], u32x4 (*slot)[64], int lane) {
+__device__ __forceinline__ void sha_schedule(uint32_t w[16], u32x4 (*slot)[kShaColumns], int lane) {
 #pragma unroll
     for (int q = 0; q < kShaBlockQuads; ++q) {
         uint32_t v[4];
@@ -468,59 +490,162 @@ __device__ __forceinline__ void sha_schedule(uint32_t w[16], u32x4 (*slot)[64], 
     }
 }
 
-// Round wave: the 64 rounds of one block from its LDS slot.
-__device__ __forceinline__ void sha_rounds(uint32_t h[8], const u32x4 (*slot)[64], int lane) {
-    uint32_t a = h[0], b = h[1], c = h[2], d = h[3], e = h[4], f = h[5], g = h[6], hh = h[7];
+// Round waves: two lanes per record.  Within each 16-lane row, banks 0 and 2
+// (lanes 0-3, 8-11) are "e-lanes" holding (e, f, g, h); banks 1 and 3 (lanes
+// 4-7, 12-15) are "a-lanes" holding (a, b, c, d) of the record four lanes
+// below them.  Both halves run one instruction stream on registers X0..X3;
+// the lane constants select what it computes:
+//   S = rotr(X0, r1) ^ rotr(X0, r2) ^ rotr(X0, r3)   Sigma1(e) | Sigma0(a)
+//   u = m ? ~(X0 ^ X1) : X0;  C = u ? X1 : X2        Ch(e,f,g) | Maj(a,b,c)
+//   W = (X3 ^ m) + K  (+ partner's X3 on e-lanes)     h + W[t]+K[t] + d | -d
+//   V = S + C + W                                    e' | Sigma0 + Maj - d
+// with m = 0 and K = W[t]+K[t] on e-lanes, m = ~0 and K = 1 on a-lanes
+// (Maj(a,b,c) = ~(a^b) ? b : c bitwise; ~d + 1 = -d).  W needs only old
+// registers, so its DPP add stays off the critical path; one DPP add then
+// finishes the round: a-lanes take e' from their partner (a' = e' + Sigma0 +
+// Maj - d = T1 + T2).  That is 10 VALU per round against 14 for one lane
+// doing both halves.
+constexpr int kDppRowShl4 = 0x104;  // lane i reads lane i + 4 of its row
+constexpr int kDppRowShr4 = 0x114;  // lane i reads lane i - 4 of its row
+constexpr int kEBanks = 0x5, kABanks = 0xA;
+
+struct ShaHalf {
+    uint32_t r1, r2, r3, m;
+};
+
+__device__ __forceinline__ uint32_t rotr_v(uint32_t x, uint32_t n) { return __builtin_amdgcn_alignbit(x, x, n); }
+// An empty asm operand: the compiler must treat x as an unknown register value
+// from here on (no constant folding of lane masks, no reassociating sums).
+__device__ __forceinline__ void opaque(uint32_t& x) { asm("" : "+v"(x)); }
+
+__device__ __forceinline__ uint32_t sha_word(const u32x4 (*slot)[kShaColumns], int column, int t) {
+    const u32x4 q = slot[t >> 2][column];
+    return (t & 3) == 0 ? q.x : (t & 3) == 1 ? q.y : (t & 3) == 2 ? q.z : q.w;
+}
+
+__device__ __forceinline__ uint32_t from_a_partner(uint32_t x) {
+    return static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(x), kDppRowShl4, 0xF, kEBanks, false));
+}
+
+__device__ __forceinline__ uint32_t from_e_partner(uint32_t x) {
+    return static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(x), kDppRowShr4, 0xF, kABanks, false));
+}
+
+// The 64 rounds of one block.  W is computed one round ahead and its first
+// term two rounds ahead, so the two instructions between V and the round's
+// DPP add are independent work (a DPP read waits two instructions after the
+// write of any register it reads).
+__device__ __forceinline__ void sha_rounds_pair(uint32_t x[4], const u32x4 (*slot)[kShaColumns], int column,
+                                                const ShaHalf& k) {
+    uint32_t x0 = x[0], x1 = x[1], x2 = x[2], x3 = x[3];
+    uint32_t z_next = (x2 ^ k.m) + sha_word(slot, column, 1);  // round 1's X3 is X2 now
+    opaque(z_next);
+    uint32_t z = (x3 ^ k.m) + sha_word(slot, column, 0);
+    opaque(z);
+    uint32_t w = from_a_partner(x3) + z;
+    opaque(w);
 #pragma unroll
-    for (int q = 0; q < kShaBlockQuads; ++q) {
-        const u32x4 wk = slot[q][lane];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const uint32_t k = i == 0 ? wk.x : i == 1 ? wk.y : i == 2 ? wk.z : wk.w;
-            const uint32_t t1 = hh + xor3(rotr(e, 6), rotr(e, 11), rotr(e, 25)) + ((e & f) | (~e & g)) + k;
-            const uint32_t t2 = xor3(rotr(a, 2), rotr(a, 13), rotr(a, 22)) + maj3(a, b, c);
-            hh = g; g = f; f = e; e = d + t1; d = c; c = b; b = a; a = t1 + t2;
+    for (int t = 0; t < 64; ++t) {
+        const uint32_t s = xor3(rotr_v(x0, k.r1), rotr_v(x0, k.r2), rotr_v(x0, k.r3));
+        // bitop3 tables index bits as (src0 << 2) | (src1 << 1) | src2.
+        const uint32_t u = __builtin_amdgcn_bitop3_b32(x0, x1, k.m, 0xD2);  // m ? ~(x0 ^ x1) : x0
+        const uint32_t c = __builtin_amdgcn_bitop3_b32(x1, x2, u, 0xE4);    // u ? x1 : x2
+        uint32_t v = s + c + w;  // e' | Sigma0 + Maj - d
+        opaque(v);
+        uint32_t z_after = 0;
+        if (t + 2 < 64) {
+            z_after = (x1 ^ k.m) + sha_word(slot, column, t + 2);  // h + W+K | -d of round t + 2
+            opaque(z_after);
         }
+        if (t + 1 < 64) {
+            w = from_a_partner(x2) + z_next;  // e-lanes add their partner's d
+            opaque(w);
+        }
+        const uint32_t next = from_e_partner(v) + v;  // a' = e' + Sigma0 + Maj - d on a-lanes
+        x3 = x2; x2 = x1; x1 = x0; x0 = next;
+        z_next = z_after;
     }
-    h[0] += a; h[1] += b; h[2] += c; h[3] += d; h[4] += e; h[5] += f; h[6] += g; h[7] += hh;
+    x[0] += x0; x[1] += x1; x[2] += x2; x[3] += x3;
+}
+
+constexpr int kShaThreads = 192;  // waves 0-1: rounds (32 records each); wave 2: message schedule (64 records)
+constexpr int kShaStep = 1;  // blocks per barrier; the producer fills one half while the rounds read the other
+
+// The producer's step for block `blk`: expand the words loaded for it, then
+// start the loads of block blk + kShaStep into the same registers.  Each of
+// the kShaStep register sets is loaded a whole step ahead of its expansion.
+template <bool kAligned>
+__device__ __forceinline__ void sha_produce(const uint8_t* __restrict__ p, uint64_t record_bytes, uint64_t whole,
+                                            int nfinal, uint64_t nblocks, uint64_t blk, uint32_t raw[16],
+                                            u32x4 (*slot)[kShaColumns], int lane) {
+    uint32_t w[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) w[i] = bswap(raw[i]);
+    if (blk + kShaStep < nblocks) sha_message_raw<kAligned>(p, record_bytes, whole, nfinal, blk + kShaStep, raw);
+    sha_schedule(w, slot, lane);
 }
 
 template <bool kAligned>
-__global__ __launch_bounds__(128) void sha256_kernel(const uint8_t* __restrict__ records, uint64_t record_bytes,
-                                                     uint64_t pitch, int64_t n_records, uint32_t* __restrict__ out) {
-    __shared__ u32x4 sched[2][kShaBlockQuads][64];
+__global__ __launch_bounds__(kShaThreads) void sha256_kernel(const uint8_t* __restrict__ records,
+                                                             uint64_t record_bytes, uint64_t pitch,
+                                                             int64_t n_records, uint32_t* __restrict__ out) {
+    __shared__ u32x4 sched[2][kShaStep][kShaBlockQuads][kShaColumns];
+    const bool producer = threadIdx.x >= 128;
     const int lane = threadIdx.x & 63;
-    const bool producer = threadIdx.x >= 64;
-    const int64_t r = static_cast<int64_t>(blockIdx.x) * 64 + lane;
+    const int bank = (lane >> 2) & 3;
+    const bool a_lane = bank & 1;
+    // Record of this lane within the workgroup's 64.
+    const int rec = producer ? lane : (threadIdx.x >> 6) * 32 + (lane >> 4) * 8 + (bank >> 1) * 4 + (lane & 3);
+    const int64_t r = static_cast<int64_t>(blockIdx.x) * 64 + rec;
     const bool live = r < n_records;
     // Lanes past the last record hash record 0 (in bounds) and store nothing.
     const uint8_t* p = records + (live ? r : 0) * pitch;
     const uint64_t whole = record_bytes / 64;
     const int nfinal = record_bytes - 64 * whole + 9 <= 64 ? 1 : 2;
     const uint64_t nblocks = whole + nfinal;
-    uint32_t w[16];
+    const uint64_t steps = (nblocks + kShaStep - 1) / kShaStep;
+    uint32_t raw[kShaStep][16];
     if (producer) {
-        sha_message<kAligned>(p, record_bytes, whole, nfinal, 0, w);
-        sha_schedule(w, sched[0], lane);
+        if (lane < 2 * kShaStep * kShaBlockQuads) {
+            const int slot = lane / kShaBlockQuads;
+            sched[slot / kShaStep][slot % kShaStep][lane % kShaBlockQuads][64] = u32x4{1u, 1u, 1u, 1u};
+        }
+#pragma unroll
+        for (int i = 0; i < kShaStep; ++i)
+            if (i < nblocks) sha_message_raw<kAligned>(p, record_bytes, whole, nfinal, i, raw[i]);
+#pragma unroll
+        for (int i = 0; i < kShaStep; ++i)
+            if (i < nblocks)
+                sha_produce<kAligned>(p, record_bytes, whole, nfinal, nblocks, i, raw[i], sched[0][i], lane);
     }
     __syncthreads();
-    uint32_t h[8] = {0x6a09e667, 0xbb67ae85, 0x3c6ef372, 0xa54ff53a, 0x510e527f, 0x9b05688c, 0x1f83d9ab, 0x5be0cd19};
-    for (uint64_t blk = 0; blk < nblocks; ++blk) {
+    ShaHalf half = a_lane ? ShaHalf{2, 13, 22, ~0u} : ShaHalf{6, 11, 25, 0u};
+    opaque(half.m);
+    uint32_t x[4];
+    if (a_lane) {
+        x[0] = 0x6a09e667; x[1] = 0xbb67ae85; x[2] = 0x3c6ef372; x[3] = 0xa54ff53a;
+    } else {
+        x[0] = 0x510e527f; x[1] = 0x9b05688c; x[2] = 0x1f83d9ab; x[3] = 0x5be0cd19;
+    }
+    const int column = a_lane ? 64 : rec;
+    for (uint64_t step = 0; step < steps; ++step) {
+        const uint64_t first = step * kShaStep;
         if (producer) {
-            if (blk + 1 < nblocks) {
-                sha_message<kAligned>(p, record_bytes, whole, nfinal, blk + 1, w);
-                sha_schedule(w, sched[(blk + 1) & 1], lane);
-            }
+#pragma unroll
+            for (int i = 0; i < kShaStep; ++i)
+                if (first + kShaStep + i < nblocks)
+                    sha_produce<kAligned>(p, record_bytes, whole, nfinal, nblocks, first + kShaStep + i, raw[i],
+                                          sched[(step + 1) & 1][i], lane);
         } else {
-            sha_rounds(h, sched[blk & 1], lane);
+#pragma unroll
+            for (int i = 0; i < kShaStep; ++i)
+                if (first + i < nblocks) sha_rounds_pair(x, sched[step & 1][i], column, half);
         }
         __syncthreads();
     }
-    if (!producer && live) {
-        u32x4* o = reinterpret_cast<u32x4*>(out + 8 * r);
-        o[0] = u32x4{bswap(h[0]), bswap(h[1]), bswap(h[2]), bswap(h[3])};
-        o[1] = u32x4{bswap(h[4]), bswap(h[5]), bswap(h[6]), bswap(h[7])};
-    }
+    if (!producer && live)
+        *reinterpret_cast<u32x4*>(out + 8 * r + (a_lane ? 0 : 4)) =
+            u32x4{bswap(x[0]), bswap(x[1]), bswap(x[2]), bswap(x[3])};
 }
 
 // ----------------------------------------------------------------- host helpers
@@ -746,10 +871,10 @@ int kvsnap_sha256_records(const void* records, uint64_t record_bytes, uint64_t r
         const auto* base = static_cast<const uint8_t*>(records);
         auto* words = reinterpret_cast<uint32_t*>(out);
         if (aligned)
-            hipLaunchKernelGGL(sha256_kernel<true>, dim3(grid), dim3(128), 0, s, base, record_bytes, record_pitch,
+            hipLaunchKernelGGL(sha256_kernel<true>, dim3(grid), dim3(kShaThreads), 0, s, base, record_bytes, record_pitch,
                                n_records, words);
         else
-            hipLaunchKernelGGL(sha256_kernel<false>, dim3(grid), dim3(128), 0, s, base, record_bytes, record_pitch,
+            hipLaunchKernelGGL(sha256_kernel<false>, dim3(grid), dim3(kShaThreads), 0, s, base, record_bytes, record_pitch,
                                n_records, words);
         check_launch("sha256");
     });

@@ -170,6 +170,22 @@ def test_crc32c_and_sha256_kernels_on_odd_record_sizes(hip_library, oracle_lib, 
             del workspace
 
 
+@pytest.mark.parametrize("n", [1, 31, 33, 64, 65, 131])
+def test_sha256_kernel_covers_every_lane_of_both_round_waves(hip_library, oracle_lib, n):
+    """Records are hashed two lanes each, 32 per round wave and 64 per workgroup: partial and full groups."""
+    record_bytes, pitch = 1000, 1008
+    data = torch.randint(0, 256, (n * pitch,), dtype=torch.uint8, device="cuda")
+    crc, sha, workspace = digest_device_records(torch, data.data_ptr(), record_bytes, pitch, n, data.device,
+                                                torch.cuda.current_stream())
+    torch.cuda.synchronize()
+    host = data.cpu().numpy()
+    for r in range(n):
+        rec = host[r * pitch: r * pitch + record_bytes].tobytes()
+        assert bytes(sha[r].cpu().numpy()) == hashlib.sha256(rec).digest(), (n, r)
+        assert (int(crc[r]) & 0xFFFFFFFF) == oracle_lib.crc32c(rec), (n, r)
+    del workspace
+
+
 def test_crc32c_kernel_extends_a_prior_value(hip_library, oracle_lib):
     lib = kernel_library()
     data = torch.randint(0, 256, (3 * 70000,), dtype=torch.uint8, device="cuda")
