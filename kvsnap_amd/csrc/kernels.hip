@@ -363,17 +363,19 @@ __global__ __launch_bounds__(64) void crc_combine_kernel(const uint32_t* __restr
 // ----------------------------------------------------------------- SHA-256 (FIPS 180-4)
 //
 // SHA-256 is a sequential chain of 64-byte compressions within a record, so
-// records are the only parallelism: one record per lane.  A wave issues one
-// VALU instruction per 4 cycles, so a record's time is its instruction count;
-// everything that does not depend on the chaining state is moved off the
-// wave that runs the rounds:
-//   * a producer wave loads each block, byte-swaps it, expands the message
-//     schedule and adds the round constants (W[t] + K[t]) into LDS, one block
-//     ahead of
-//   * the round wave, which runs only the 64 rounds (about 14 VALU each).
-// Three-input XORs and Maj are single v_bitop3_b32 instructions (truth tables
-// 0x96 and 0xE8, both symmetric in their inputs).  Workgroup = one round wave
-// + one producer wave over the same 64 records.
+// records are the only parallelism, and a few hundred records fill only a few
+// dozen of the chip's 1024 SIMDs.  A record's time is therefore the issue time
+// of its chain (a wave64 VALU instruction takes 4 cycles of its SIMD), and
+// everything that does not depend on the chaining state is moved off it:
+//   * a producer wave (one record per lane) loads each block a step ahead,
+//     byte-swaps it, expands the message schedule and adds the round
+//     constants (W[t] + K[t]) into LDS;
+//   * two round waves run only the 64 rounds, two lanes per record (the
+//     e-half and the a-half of each round side by side; see sha_rounds_pair),
+//     10 VALU per round.
+// Workgroup = two round waves + one producer wave over the same 64 records;
+// the producer fills one half of a double buffer of kShaStep blocks while the
+// round waves read the other.
 
 __constant__ uint32_t kSha[64] = {
     0x428a2f98, 0x71374491, 0xb5c0fbcf, 0xe9b5dba5, 0x3956c25b, 0x59f111f1, 0x923f82a4, 0xab1c5ed5,
@@ -569,7 +571,7 @@ __device__ __forceinline__ void sha_rounds_pair(uint32_t x[4], const u32x4 (*slo
 }
 
 constexpr int kShaThreads = 192;  // waves 0-1: rounds (32 records each); wave 2: message schedule (64 records)
-constexpr int kShaStep = 1;  // blocks per barrier; the producer fills one half while the rounds read the other
+constexpr int kShaStep = 2;  // blocks per barrier; the producer fills one half while the rounds read the other
 
 // The producer's step for block `blk`: expand the words loaded for it, then
 // start the loads of block blk + kShaStep into the same registers.  Each of
@@ -612,10 +614,10 @@ __global__ __launch_bounds__(kShaThreads) void sha256_kernel(const uint8_t* __re
         }
 #pragma unroll
         for (int i = 0; i < kShaStep; ++i)
-            if (i < nblocks) sha_message_raw<kAligned>(p, record_bytes, whole, nfinal, i, raw[i]);
+            if (static_cast<uint64_t>(i) < nblocks) sha_message_raw<kAligned>(p, record_bytes, whole, nfinal, i, raw[i]);
 #pragma unroll
         for (int i = 0; i < kShaStep; ++i)
-            if (i < nblocks)
+            if (static_cast<uint64_t>(i) < nblocks)
                 sha_produce<kAligned>(p, record_bytes, whole, nfinal, nblocks, i, raw[i], sched[0][i], lane);
     }
     __syncthreads();
