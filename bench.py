@@ -27,6 +27,11 @@ Other workloads (one JSON line each, for the record; not the headline):
     --workload rotating-fp8   Qwen3-1.7B fp8-e4m3 sessions of 1k/2k/4k/8k tokens
                               saved and restored round-robin beside a synthetic
                               16-sequence decode on the compute stream
+    --workload turns          an 8192-token Qwen3-8B session growing by 512
+                              tokens a turn, each turn end saved into the host
+                              tier in full (every block gathered and hashed, as
+                              the reference rehashes every block) and by delta
+                              (only the blocks past the unchanged prefix)
     --workload kernels        each kernel alone plus a plain copy of known size
                               (the driver for rocprofv3 counter runs)
 """
@@ -563,18 +568,117 @@ def run_kernels(args):
             "note": "restore_kernel reads pinned host records (link) and writes HBM; bytes counted both ways"}
 
 
+# ---------------------------------------------------------------- multi-turn host-tier saves
+
+def run_turns(args):
+    import torch
+    from kvsnap_amd import synth
+    from kvsnap_amd.dataplane import TorchBlockDataPlane
+    from kvsnap_amd.host_tier import HostTier
+
+    layers, num_blocks, block_size = 36, 16384, 16
+    start_tokens, turn_tokens, turns = 8192, 512, args.turns
+    final = (start_tokens + turns * turn_tokens) // block_size
+    caches, backing = synth.make_caches(layers, num_blocks, block_size=block_size, layout=args.layout)
+    size = layers * 65536
+    # Both tiers hold one snapshot, and a save reserves its fresh blocks before adopting them.
+    plane = TorchBlockDataPlane(caches, block_size, 4 * final * size + (64 << 20))
+    plane.warm_up()
+    keep = synth.fill(plane, 0)
+    torch.cuda.synchronize()
+    del keep
+    ids = random.Random(1).sample(range(1, num_blocks), final)
+    full, delta = HostTier(plane, 2 * final * size), HostTier(plane, 2 * final * size)
+    prev_full = prev_delta = None
+    rows = []
+    for turn in range(turns + 1):
+        tokens = start_tokens + turn * turn_tokens
+        count = tokens // block_size
+        if turn:
+            # The turn's new tokens: fresh content in its new blocks.
+            first = (tokens - turn_tokens) // block_size
+            keep = [synth.fill(plane, 1000 + turn, first_block=b, num_blocks=1) for b in ids[first:count]]
+            torch.cuda.synchronize()
+            del keep
+        fence_full, fence_delta = Stamp(), Stamp()
+        t0 = time.perf_counter()
+        snap_full = full.save(ids[:count], tokens, fenced=fence_full)
+        t1 = time.perf_counter()
+        snap_delta = delta.save(ids[:count], tokens, previous=prev_delta, fenced=fence_delta)
+        t2 = time.perf_counter()
+        if snap_full["segments"] != snap_delta["segments"]:
+            raise RuntimeError(f"turn {turn}: the delta save's segments differ from the full save's")
+        rows.append(dict(turn=turn, tokens=tokens, blocks=count,
+                         full_fenced_ms=round((fence_full.at - t0) * 1e3, 2), full_ms=round((t1 - t0) * 1e3, 2),
+                         full_gathered=full.gathered_blocks,
+                         delta_fenced_ms=round((fence_delta.at - t1) * 1e3, 2), delta_ms=round((t2 - t1) * 1e3, 2),
+                         delta_gathered=delta.gathered_blocks))
+        log(f"turn {turn}: {tokens} tokens; full: fenced {rows[-1]['full_fenced_ms']} ms, adopted "
+            f"{rows[-1]['full_ms']} ms; delta ({delta.gathered_blocks} blocks): fenced "
+            f"{rows[-1]['delta_fenced_ms']} ms, adopted {rows[-1]['delta_ms']} ms")
+        for tier, previous in ((full, prev_full), (delta, prev_delta)):
+            if previous is not None:
+                tier.release(previous)
+        prev_full, prev_delta = snap_full, snap_delta
+    cpu = None if args.no_cpu_baseline else turn_cpu_baseline(full, prev_full, size)
+    later = rows[1:]
+    median = lambda key: statistics.median(r[key] for r in later)
+    for tier, previous in ((full, prev_full), (delta, prev_delta)):
+        tier.release(previous)
+    plane.close()
+    return {"metric": "turn-end host-tier save of a growing Qwen3-8B session: ms until the GPU blocks are free "
+                      "(D2H fenced), delta save",
+            "workload": "turns", "value": median("delta_fenced_ms"), "unit": "ms", "higher_is_better": False,
+            "full_fenced_ms": median("full_fenced_ms"), "delta_adopted_ms": median("delta_ms"),
+            "full_adopted_ms": median("full_ms"),
+            "fence_speedup": round(median("full_fenced_ms") / median("delta_fenced_ms"), 2),
+            "note": "adopted = digests computed on the GPU and the blocks held by content id; a record's "
+                    "SHA-256 is one sequential chain, so both saves' adoption waits about one record's hash",
+            "record_bytes": size, "start_tokens": start_tokens, "tokens_per_turn": turn_tokens, "turns": rows,
+            "segments_equal": True, "layout": args.layout, "cpu_baseline": cpu}
+
+
+class Stamp:
+    """A ``fenced`` event that records when it was set."""
+    at = None
+
+    def set(self):
+        self.at = time.perf_counter()
+
+
+def turn_cpu_baseline(tier, snapshot, size):
+    """The reference's turn-end rehash (volatile.py:226-229): SHA-256 + CRC32C of every block, 8 threads.
+
+    Timed by the oracle on this host's cores over the last turn's held
+    blocks, in place in pinned memory.
+    """
+    from concurrent.futures import ThreadPoolExecutor
+    import oracle
+    oracle.build()
+    oracle.sha256_select(True)
+    pointers = [tier._entries[s["blob_id"]]["allocation"].pointer for s in snapshot["segments"]]
+    with ThreadPoolExecutor(max_workers=8) as pool:
+        t0 = time.perf_counter()
+        list(pool.map(lambda p: oracle.digest_records(p, size, size, 1, threads=1), pointers))
+        elapsed = time.perf_counter() - t0
+    return {"value": round(elapsed * 1e3, 2), "unit": "ms", "cores": 8, "kind": "port",
+            "gbps": round(len(pointers) * size / elapsed / 1e9, 2),
+            "sample": f"the last turn's {len(pointers)} held blocks x {size} B, SHA-256 + CRC32C each"}
+
+
 def main():
     parser = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     parser.add_argument("--gpus", type=int, default=1)
     parser.add_argument("--steps", type=int, default=10)
     parser.add_argument("--warmup", type=int, default=3)
     parser.add_argument("--layout", choices=("kv_split", "vllm"), default="kv_split")
-    parser.add_argument("--workload", choices=("save-restore", "disk-fork", "rotating-fp8", "kernels"),
+    parser.add_argument("--workload", choices=("save-restore", "disk-fork", "rotating-fp8", "turns", "kernels"),
                         default="save-restore")
     parser.add_argument("--reps", type=int, default=5, help="kernels: timed repetitions per kernel")
     parser.add_argument("--hash-depth", type=int, default=2,
                         help="save-restore: steps a save's digests may trail before they are collected")
     parser.add_argument("--rounds", type=int, default=4, help="rotating-fp8: rounds over the four sessions")
+    parser.add_argument("--turns", type=int, default=6, help="turns: turns after the first save")
     parser.add_argument("--disk-dir", default=None, help="disk-fork: where the blob files go")
     parser.add_argument("--cpu-seconds", type=float, default=20.0)
     parser.add_argument("--no-cpu-baseline", action="store_true")
@@ -586,7 +690,7 @@ def main():
     import torch
     torch.cuda.set_device(0)
     runner = {"save-restore": run_save_restore, "disk-fork": run_disk_fork, "rotating-fp8": run_rotating,
-              "kernels": run_kernels}
+              "turns": run_turns, "kernels": run_kernels}
     print(json.dumps(runner[args.workload](args)), flush=True)
 
 

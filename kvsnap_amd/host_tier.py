@@ -162,13 +162,16 @@ class HostTier:
 
     # ------------------------------------------------------------- data path
 
-    def save(self, block_ids, num_kv_tokens, *, previous=None, chunk_bytes=64 << 20):
+    def save(self, block_ids, num_kv_tokens, *, previous=None, chunk_bytes=64 << 20, fenced=None):
         """Save a session's blocks into the tier; returns the snapshot (held until :meth:`release`).
 
         With ``previous`` (a snapshot of this session saved or restored into
         the same block ids), the unchanged prefix is taken from it, and only
         the rest is gathered, copied to pinned memory and hashed on the GPU.
         The segments equal those of a full save of the same blocks.
+        ``fenced.set()`` is called once the copies to pinned memory are done
+        and the GPU blocks may be freed, before the hashes are waited for
+        (the reference's save job, ``vllm.py:601-608``).
         """
         plane = self.plane
         block_size, size = plane.block_size, plane.block_bytes
@@ -194,6 +197,8 @@ class HostTier:
             # still be using it), as the reference's save does (vllm.py:602-607).
             plane.save_gather(fresh, [(allocation, 0) for allocation in allocations],
                               num_kv_tokens - keep * block_size, chunk_bytes=chunk_bytes, digests=digests)
+        if fenced is not None:
+            fenced.set()
         ids = digests[0].result() if fresh else []
         self.gathered_blocks = len(fresh)
         segments = self.adopt(allocations, ids, reuse=reuse)
