@@ -396,6 +396,40 @@ def test_qwen3_1_7b_round_trip_at_the_cpu_reference_shape(planes, oracle_lib):
     staged.close()
 
 
+def test_qwen3_8b_8k_session_at_full_size(planes, oracle_lib):
+    """The headline workload's shape: 36 K/V-split layers in a 16384-block cache (36 GiB), an 8192-token
+    session of 512 records (1,207,959,552 bytes).  Save with GPU digests, restore into a fresh table: the
+    round trip is the identity, and every CRC32C and SHA-256 equals the oracle's over the pinned records."""
+    caches, backing = synth.make_caches(36, 16384, layout="kv_split")
+    size = 36 * 65536
+    plane = planes(caches, capacity=512 * size + (64 << 20))
+    keep = synth.fill(plane, 0)
+    torch.cuda.synchronize()
+    del keep
+    assert plane.block_bytes == size == 2359296
+    saved, restored = synth.block_tables(16384, 512)
+    assert max(saved + restored) < 16384
+    staged = plane.pool.reserve(512 * size)
+    targets = [(staged, i * size) for i in range(512)]
+    digests = []
+    plane.save_gather(saved, targets, 8192, digests=digests)
+    got = digests[0].result()
+    crcs, shas = oracle_lib.digest_records(staged.pointer, size, size, 512, threads=16)
+    assert [crc for _, crc in got] == crcs.tolist()
+    assert [sha for sha, _ in got] == [bytes(s).hex() for s in shas]
+    for index in (0, 301, 511):
+        record = pinned_bytes(staged, index * size, size)
+        for s, (offset, _, _, nbytes) in enumerate(plane.spans()):
+            assert np.array_equal(record[offset:offset + nbytes],
+                                  oracle_lib.fill_span(0, s, saved[index], nbytes, synth.KIND_BF16)), (index, s)
+    assert plane.load_scatter(restored, targets) == 19
+    torch.cuda.synchronize()
+    src, dst = torch.tensor(saved, device="cuda"), torch.tensor(restored, device="cuda")
+    for view in caches.values():               # [2, blocks, N, H, D]
+        assert torch.equal(view[:, src].view(torch.int16), view[:, dst].view(torch.int16))
+    staged.close()
+
+
 @pytest.mark.parametrize("seed", range(6))
 def test_copy_kernels_on_random_span_tables_including_8_byte_alignment(hip_library, oracle_lib, seed):
     """Random geometries: odd word counts, pitches that are odd multiples of 8 bytes, bases offset by 8,
