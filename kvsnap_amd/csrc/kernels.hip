@@ -23,9 +23,9 @@
 // int64 arrays in device memory, as in the reference's launch contract.
 //
 // No MFMA anywhere: nothing on this path is a contraction.  The copies are
-// 16-byte-per-lane streams (one dwordx4 per lane, 8 in flight per lane), the
-// CRC is LDS table lookups combined in GF(2), and SHA-256 is one record per
-// lane because the hash is a sequential chain within a record.
+// 16-byte-per-lane streams (4 or 8 dwordx4 loads in flight per lane), the CRC
+// is LDS table lookups combined in GF(2), and SHA-256 runs one record per two
+// lanes because the hash is a sequential chain within a record.
 #include <hip/hip_runtime.h>
 
 #include "common.h"
@@ -269,11 +269,14 @@ __global__ __launch_bounds__(kThreads) void synth_decode_kernel(const int64_t* _
 // combined by Horner's rule; crc32c = ~(shift(~prior, N) ^ R(record)).
 //
 // Inside a stripe, lane t of a 256-lane workgroup reads the 16-byte word at
-// t*16 of every 4 KiB group (fully coalesced), folds it with
+// t*16 of every 4 KiB group (fully coalesced; all of the stripe's words are
+// loaded before any is folded, so a lane has 16 loads in flight), folds them
+// with
 //   acc = shift(acc, 4096) ^ R16(word),
 // and finally contributes shift(acc, (255 - t) * 16); the workgroup's XOR of
 // those is the stripe's raw CRC.  Tables (in LDS):
-//   T[k][v]  = shift(v, 4 - k)             slicing-by-4 for R16,
+//   T[i][v]  = shift(v, 16 - i)            slicing-by-16 for R16: byte i of
+//                                          the word, 16 independent lookups,
 //   G[k][v]  = shift(v << 8k, 4096)        the per-group advance.
 // Per-lane constants M[t] = x^(8 * 16 * (255 - t)) mod P are applied with a
 // bitwise GF(2) multiply.
@@ -283,7 +286,10 @@ constexpr int kGroup = kThreads * 16;  // bytes per group
 constexpr int kStripeGroups = 16;      // groups per stripe: 64 KiB stripes
 constexpr int kCrcGrid = 2048;         // persistent workgroups
 
-__device__ uint32_t g_crc_tables[256 * 4 + 256 * 4 + 256];
+constexpr int kCrcAdvance = 256 * 16;            // G's offset in g_crc_tables
+constexpr int kCrcLaneShift = kCrcAdvance + 256 * 4; // M's offset
+
+__device__ uint32_t g_crc_tables[kCrcLaneShift + kThreads];
 
 __device__ __forceinline__ uint32_t gf_mul(uint32_t a, uint32_t b) {
     // a * b mod P in the reflected representation (bit 31 is x^0).
@@ -300,50 +306,57 @@ __device__ __forceinline__ uint32_t slice4(const uint32_t (*t)[256], uint32_t x)
     return t[0][x & 0xFF] ^ t[1][(x >> 8) & 0xFF] ^ t[2][(x >> 16) & 0xFF] ^ t[3][x >> 24];
 }
 
+__device__ __forceinline__ uint32_t fold16(const uint32_t (*t)[256], u32x4 v) {
+    uint32_t s = 0;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) s ^= t[k][(v.x >> (8 * k)) & 0xFF] ^ t[4 + k][(v.y >> (8 * k)) & 0xFF];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) s ^= t[8 + k][(v.z >> (8 * k)) & 0xFF] ^ t[12 + k][(v.w >> (8 * k)) & 0xFF];
+    return s;
+}
+
 template <bool kAligned>
 __global__ __launch_bounds__(kThreads) void crc_stripes_kernel(const uint8_t* __restrict__ records, uint64_t pitch,
                                                               int64_t n_records, int64_t stripes, int64_t groups,
                                                               uint64_t pad, uint32_t* __restrict__ partial) {
-    __shared__ uint32_t t4[4][256];
+    __shared__ uint32_t t16[16][256];
     __shared__ uint32_t tg[4][256];
     __shared__ uint32_t red[kThreads / 64];
-    for (int i = threadIdx.x; i < 1024; i += kThreads) {
-        t4[i >> 8][i & 255] = g_crc_tables[i];
-        tg[i >> 8][i & 255] = g_crc_tables[1024 + i];
-    }
-    const uint32_t lane_shift = g_crc_tables[2048 + threadIdx.x];
+    for (int i = threadIdx.x; i < 4096; i += kThreads) t16[i >> 8][i & 255] = g_crc_tables[i];
+    for (int i = threadIdx.x; i < 1024; i += kThreads) tg[i >> 8][i & 255] = g_crc_tables[kCrcAdvance + i];
+    const uint32_t lane_shift = g_crc_tables[kCrcLaneShift + threadIdx.x];
     __syncthreads();
     const int64_t jobs = n_records * stripes;
     const int64_t stripe_bytes = groups * kGroup;
     for (int64_t job = blockIdx.x; job < jobs; job += gridDim.x) {
         const int64_t r = job / stripes, j = job - r * stripes;
         const uint8_t* rec = records + r * pitch;
-        uint32_t acc = 0;
-        for (int64_t g = 0; g < groups; ++g) {
-            const int64_t virt = j * stripe_bytes + g * kGroup + threadIdx.x * 16;
-            const int64_t at = virt - static_cast<int64_t>(pad);
-            uint32_t w0 = 0, w1 = 0, w2 = 0, w3 = 0;
-            if (kAligned) {
-                if (at >= 0) {
-                    const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(rec + at));
-                    w0 = v.x; w1 = v.y; w2 = v.z; w3 = v.w;
-                }
-            } else {
-                uint32_t w[4] = {0, 0, 0, 0};
-                for (int k = 0; k < 16; ++k)
-                    if (at + k >= 0) w[k >> 2] |= static_cast<uint32_t>(rec[at + k]) << (8 * (k & 3));
-                w0 = w[0]; w1 = w[1]; w2 = w[2]; w3 = w[3];
-            }
-            uint32_t s = slice4(t4, w0);
-            s = slice4(t4, s ^ w1);
-            s = slice4(t4, s ^ w2);
-            s = slice4(t4, s ^ w3);
-            acc = slice4(tg, acc) ^ s;
-        }
-        uint32_t v = gf_mul(lane_shift, acc);
+        // groups is 1 or kStripeGroups; bytes before the record (front padding) are zero.
+        u32x4 v[kStripeGroups];
 #pragma unroll
-        for (int o = 32; o > 0; o >>= 1) v ^= __shfl_xor(v, o);
-        if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+        for (int g = 0; g < kStripeGroups; ++g) {
+            v[g] = u32x4{0u, 0u, 0u, 0u};
+            const int64_t at = j * stripe_bytes + g * kGroup + threadIdx.x * 16 - static_cast<int64_t>(pad);
+            if (g < groups) {
+                if (kAligned) {
+                    // The padding is a multiple of 16 here, so a word is all padding or all record.
+                    if (at >= 0) v[g] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(rec + at));
+                } else {
+                    uint32_t w[4] = {0, 0, 0, 0};
+                    for (int k = 0; k < 16; ++k)
+                        if (at + k >= 0) w[k >> 2] |= static_cast<uint32_t>(rec[at + k]) << (8 * (k & 3));
+                    v[g] = u32x4{w[0], w[1], w[2], w[3]};
+                }
+            }
+        }
+        uint32_t acc = 0;
+#pragma unroll
+        for (int g = 0; g < kStripeGroups; ++g)
+            if (g < groups) acc = slice4(tg, acc) ^ fold16(t16, v[g]);
+        uint32_t x = gf_mul(lane_shift, acc);
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) x ^= __shfl_xor(x, o);
+        if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = x;
         __syncthreads();
         if (threadIdx.x == 0) partial[job] = red[0] ^ red[1] ^ red[2] ^ red[3];
         __syncthreads();
@@ -685,14 +698,15 @@ void ensure_crc_tables() {
         throw std::runtime_error("no current HIP device for the CRC32C tables");
     std::lock_guard<std::mutex> lock(g_table_mutex);
     if (g_tables_ready[device]) return;
-    static uint32_t tables[256 * 4 + 256 * 4 + 256];
+    static uint32_t tables[kCrcLaneShift + kThreads];
+    for (uint32_t i = 0; i < 16; ++i) {
+        const uint32_t m = host_xpow8n(16 - i);
+        for (uint32_t v = 0; v < 256; ++v) tables[256 * i + v] = host_gf_mul(m, v);
+    }
     const uint32_t group_shift = host_xpow8n(kGroup);
     for (uint32_t k = 0; k < 4; ++k)
-        for (uint32_t v = 0; v < 256; ++v) {
-            tables[256 * k + v] = host_shift(v, 4 - k);
-            tables[1024 + 256 * k + v] = host_gf_mul(group_shift, v << (8 * k));
-        }
-    for (uint32_t t = 0; t < 256; ++t) tables[2048 + t] = host_xpow8n(16ull * (255 - t));
+        for (uint32_t v = 0; v < 256; ++v) tables[kCrcAdvance + 256 * k + v] = host_gf_mul(group_shift, v << (8 * k));
+    for (uint32_t t = 0; t < kThreads; ++t) tables[kCrcLaneShift + t] = host_xpow8n(16ull * (kThreads - 1 - t));
     hipError_t rc = hipMemcpyToSymbol(HIP_SYMBOL(g_crc_tables), tables, sizeof tables, 0, hipMemcpyHostToDevice);
     if (rc != hipSuccess) throw std::runtime_error(std::string("CRC32C table upload: ") + hipGetErrorString(rc));
     g_tables_ready[device] = true;
