@@ -173,7 +173,7 @@ def same_blocks(torch, caches, a, b):
 def run_save_restore(args):
     import torch
     from kvsnap_amd import synth
-    from kvsnap_amd.dataplane import KernelTimer, TorchBlockDataPlane
+    from kvsnap_amd.dataplane import KernelTimer, TorchBlockDataPlane, gather_blocks, scatter_blocks
     from kvsnap_amd.ordering import early_launch_index
 
     layers, num_blocks, block_size, tokens = 36, 16384, 16, 8192
@@ -266,6 +266,18 @@ def run_save_restore(args):
     gather_achieved = 2 * total / (gather["avg_ms"] * 1e6)          # read + write, one launch per save
     restore_link = (total * args.steps / restore["launches"]) / (restore["avg_ms"] * 1e6)
     crc_achieved = total / (crc["avg_ms"] * 1e6)
+    # The scatter from device records (the verified restore's last step), after the timed region: the
+    # session's records gathered into device memory, then scattered into the restore targets, which
+    # already hold the same bytes.
+    records = torch.empty(total, dtype=torch.uint8, device="cuda")
+    tables = plane._load_tables()
+    src_ids = torch.tensor(source, dtype=torch.int64, device="cuda")
+    dst_ids = torch.tensor(target, dtype=torch.int64, device="cuda")
+    gather_blocks(src_ids, *tables, records.data_ptr(), size)
+    scatter_ms = median_ms(torch, torch.cuda.current_stream(),
+                           lambda: scatter_blocks(records.data_ptr(), size, dst_ids, *tables), reps=5)
+    del records
+    scatter_achieved = 2 * total / (scatter_ms * 1e6)
     cpu = None if args.no_cpu_baseline else cpu_baseline(layers, 65536, args.cpu_seconds)
     out = {
         "metric": "8k Qwen3-8B KV restore/save GB/s and ms; % of host-link and HBM roofline",
@@ -303,6 +315,9 @@ def run_save_restore(args):
                      "traffic_source": "profiles/qwen3-8b-8k-kernels.traffic.md (rocprofv3 FETCH_SIZE, WRITE_SIZE)"},
         "link_roofline": {"kernel": "restore_kernel", "bound": "host-link", "achieved": round(restore_link, 2),
                           "peak": round(h2d_peak, 2), "unit": "GB/s", "frac": round(restore_link / h2d_peak, 4)},
+        "scatter_roofline": {"kernel": "scatter_kernel (device records to cache)", "bound": "hbm",
+                             "achieved": round(scatter_achieved, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                             "frac": round(scatter_achieved / HBM_PEAK_GBPS, 4), "ms": round(scatter_ms, 4)},
         "crc_roofline": {"kernel": "crc_stripes_kernel", "bound": "hbm", "achieved": round(crc_achieved, 1),
                          "peak": HBM_PEAK_GBPS, "unit": "GB/s", "frac": round(crc_achieved / HBM_PEAK_GBPS, 4)},
         "sha256": {"kernel": "sha256_kernel", "ms": round(sha["avg_ms"], 3),
@@ -524,7 +539,7 @@ def run_kernels(args):
     import torch
     from kvsnap_amd import synth
     from kvsnap_amd.dataplane import (_check, copy_host_blocks, digest_device_records, gather_blocks,
-                                      kernel_library, TorchBlockDataPlane)
+                                      kernel_library, scatter_blocks, TorchBlockDataPlane)
 
     layers, num_blocks, block_size, tokens = 36, 16384, 16, 8192
     session = tokens // block_size
@@ -557,6 +572,8 @@ def run_kernels(args):
             stage.data_ptr(), size, size, session, 0, crc.data_ptr(), work.data_ptr(), work_bytes,
             stream.cuda_stream)), total, args.reps),
         "restore_kernel": (lambda: copy_host_blocks(pinned, dst, *tables), 2 * total, args.reps),
+        # The verified restore's scatter: records in device staging, one workgroup per (block, span).
+        "scatter_kernel": (lambda: scatter_blocks(stage.data_ptr(), size, dst, *tables), 2 * total, args.reps),
         "sha256_kernel": (lambda: _check(lib, lib.kvsnap_sha256_records(
             stage.data_ptr(), size, size, session, sha.data_ptr(), stream.cuda_stream)), total, 1),
     }

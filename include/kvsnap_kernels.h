@@ -45,6 +45,15 @@ int kvsnap_gather_blocks(const int64_t* blocks, int64_t n_blocks, const int64_t*
                          const int64_t* span_bases, const int64_t* span_pitches, const int64_t* span_words,
                          int64_t n_spans, void* records, int64_t record_pitch, int programs, uintptr_t stream);
 
+/* Scatter: the record at records + i * record_pitch, in device memory, into
+ * block blocks[i]'s spans; the gather's inverse.  The last step of a restore
+ * whose records were first staged and CRC-checked on the device: replaces the
+ * reference's restore launch (kvsnap/connector/copy_kernel.py:43-49) for
+ * device-resident sources, with an HBM-to-HBM grid shape. */
+int kvsnap_scatter_blocks(const void* records, int64_t record_pitch, const int64_t* blocks, int64_t n_blocks,
+                          const int64_t* span_offsets, const int64_t* span_bases, const int64_t* span_pitches,
+                          const int64_t* span_words, int64_t n_spans, int programs, uintptr_t stream);
+
 /* Zero n byte ranges [base + offsets[i], + lengths[i]): the token slots past
  * the last computed token of a record.  Replaces the host memsets of
  * TorchBlockDataPlane._zero_tail, kvsnap/connector/dataplane.py:262-272. */

@@ -82,6 +82,8 @@ constexpr int kRestoreThreads = 256, kRestoreUnroll = 8;
 // Gather: HBM to HBM, one 1024-lane workgroup per (block, span) job with 4
 // loads in flight per lane (64 KiB per pass), the fastest shape measured.
 constexpr int kGatherThreads = 1024, kGatherUnroll = 4;
+// Scatter from device records: HBM to HBM like the gather, writes scattered.
+constexpr int kScatterThreads = 1024, kScatterUnroll = 4;
 
 __global__ __launch_bounds__(kRestoreThreads) void restore_kernel(
     const int64_t* __restrict__ sources, const int64_t* __restrict__ blocks, int64_t n_blocks,
@@ -106,6 +108,21 @@ __global__ __launch_bounds__(kGatherThreads) void gather_kernel(
         const char* src = reinterpret_cast<const char*>(bases[s] + blocks[b] * pitches[s]);
         char* dst = records + b * record_pitch + offs[s];
         copy_span<kGatherThreads, kGatherUnroll>(src, dst, words[s] * 8);
+    }
+}
+
+// Scatter from packed records in device memory (HBM to HBM, the verified
+// restore's last step): the gather's inverse, with its shape.
+__global__ __launch_bounds__(kScatterThreads) void scatter_kernel(
+    const char* __restrict__ records, int64_t record_pitch, const int64_t* __restrict__ blocks, int64_t n_blocks,
+    const int64_t* __restrict__ offs, const int64_t* __restrict__ bases, const int64_t* __restrict__ pitches,
+    const int64_t* __restrict__ words, int64_t n_spans) {
+    const int64_t jobs = n_blocks * n_spans;
+    for (int64_t job = blockIdx.x; job < jobs; job += gridDim.x) {
+        const int64_t b = job / n_spans, s = job - b * n_spans;
+        const char* src = records + b * record_pitch + offs[s];
+        char* dst = reinterpret_cast<char*>(bases[s] + blocks[b] * pitches[s]);
+        copy_span<kScatterThreads, kScatterUnroll>(src, dst, words[s] * 8);
     }
 }
 
@@ -767,6 +784,21 @@ int kvsnap_restore_blocks(const int64_t* sources, const int64_t* blocks, int64_t
                            reinterpret_cast<hipStream_t>(stream), sources, blocks, n_blocks, span_offsets,
                            span_bases, span_pitches, span_words, n_spans);
         check_launch("restore");
+    });
+}
+
+int kvsnap_scatter_blocks(const void* records, int64_t record_pitch, const int64_t* blocks, int64_t n_blocks,
+                          const int64_t* span_offsets, const int64_t* span_bases, const int64_t* span_pitches,
+                          const int64_t* span_words, int64_t n_spans, int programs, uintptr_t stream) {
+    return guard([&] {
+        if (n_blocks < 0 || n_spans < 0 || record_pitch < 0) throw std::runtime_error("negative scatter size");
+        if (n_blocks == 0 || n_spans == 0) return;
+        if (!records || !blocks || !span_offsets || !span_bases || !span_pitches || !span_words)
+            throw std::runtime_error("scatter tables must be device pointers");
+        hipLaunchKernelGGL(scatter_kernel, dim3(grid_for(n_blocks * n_spans, programs)), dim3(kScatterThreads), 0,
+                           reinterpret_cast<hipStream_t>(stream), static_cast<const char*>(records), record_pitch,
+                           blocks, n_blocks, span_offsets, span_bases, span_pitches, span_words, n_spans);
+        check_launch("scatter");
     });
 }
 

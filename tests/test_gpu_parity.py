@@ -433,7 +433,7 @@ def test_qwen3_8b_8k_session_at_full_size(planes, oracle_lib):
 @pytest.mark.parametrize("seed", range(6))
 def test_copy_kernels_on_random_span_tables_including_8_byte_alignment(hip_library, oracle_lib, seed):
     """Random geometries: odd word counts, pitches that are odd multiples of 8 bytes, bases offset by 8,
-    so the kernels' 8-byte path runs beside the 16-byte one; gather, restore and gather-to-records."""
+    so the kernels' 8-byte path runs beside the 16-byte one; gather, restore, scatter and gather-to-records."""
     rng = np.random.default_rng(100 + seed)
     blocks = int(rng.integers(4, 40))
     n_spans = int(rng.integers(1, 9))
@@ -485,6 +485,16 @@ def test_copy_kernels_on_random_span_tables_including_8_byte_alignment(hip_libra
     torch.cuda.synchronize()
     after = [s.cpu().numpy() for s in stores]
     oracle_lib.scatter(spans, targets, [expected[i].ctypes.data for i in range(count)])
+    for a, h in zip(after, host_before):
+        assert np.array_equal(a, h)
+    # scatter the same device records (record pitch, 8-byte offset) into a third set of blocks
+    third = rng.choice(blocks, count, replace=False).tolist()
+    _check(lib, lib.kvsnap_scatter_blocks(out.data_ptr() + 8, record_words * 8, dev(third).data_ptr(), count,
+                                          offs.data_ptr(), bases.data_ptr(), pitch_b.data_ptr(), words_t.data_ptr(),
+                                          n_spans, 3, stream))
+    torch.cuda.synchronize()
+    after = [s.cpu().numpy() for s in stores]
+    oracle_lib.scatter(spans, third, [expected[i].ctypes.data for i in range(count)])
     for a, h in zip(after, host_before):
         assert np.array_equal(a, h)
 
