@@ -522,6 +522,14 @@ def test_pipelined_disk_restore_is_byte_exact_and_refuses_corrupt_blobs(planes, 
     assert launches == 4 and progress[0] == (None, 20 * size) and progress[-1][1] == 0
     assert [left for _, left in progress[1:]] == [14 * size, 8 * size, 2 * size, 0]
     assert np.array_equal(host_copy(backing), expected)
+    # again through a pool that holds two 3-block chunks: the staging ring, not the snapshot, sizes it
+    small = planes(caches, capacity=6 * size + (1 << 20))
+    targets = torch.tensor(restored, device="cuda")
+    for view in caches.values():              # [2, blocks, N, H, D]; ids < 48
+        view[:, targets] = 0
+    assert small.load_from_disk(restored, store, segments, chunk_bytes=3 * size, workers=2, verify=verify,
+                                ring=2) == 7
+    assert np.array_equal(host_copy(backing), expected)
     # a flipped payload bit in the third chunk's blob
     path = store.path(segments[13]["blob_id"])
     raw = bytearray(path.read_bytes())
