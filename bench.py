@@ -32,12 +32,19 @@ Other workloads (one JSON line each, for the record; not the headline):
                               tier in full (every block gathered and hashed, as
                               the reference rehashes every block) and by delta
                               (only the blocks past the unchanged prefix)
+    --workload cpu-roundtrip  the reference's CPU-runnable case (Qwen3-1.7B shape,
+                              4096-block cache, 2048-token session): gather,
+                              CRC32C, scatter, compare -- on the host cores
+                              (the reference's path, restated by the oracle)
+                              and on the GPU on the same bytes, the GPU
+                              restore checked against the CPU's CRC32Cs
     --workload kernels        each kernel alone plus a plain copy of known size
                               (the driver for rocprofv3 counter runs)
 """
 from __future__ import annotations
 
 import argparse
+import ctypes
 import json
 import os
 import random
@@ -590,6 +597,103 @@ def run_kernels(args):
             "note": "restore_kernel reads pinned host records (link) and writes HBM; bytes counted both ways"}
 
 
+# ---------------------------------------------------------------- the reference's CPU round trip
+
+def run_cpu_roundtrip(args):
+    import numpy as np
+    import torch
+    import oracle
+    from kvsnap_amd import synth
+    from kvsnap_amd.dataplane import TorchBlockDataPlane
+
+    layers, num_blocks, block_size, tokens = 28, 4096, 16, 2048
+    session = tokens // block_size
+    caches, backing = synth.make_caches(layers, num_blocks, block_size=block_size, layout=args.layout)
+    plane = TorchBlockDataPlane(caches, block_size, session * layers * 65536 + (64 << 20))
+    plane.warm_up()
+    keep = synth.fill(plane, 0)
+    torch.cuda.synchronize()
+    del keep
+    size = plane.block_bytes
+    total = session * size
+    source, target = synth.block_tables(num_blocks, session)
+
+    # CPU leg: a host cache of the same geometry; the source blocks hold the bytes the GPU cache holds (the
+    # oracle's generator is the GPU's, bit for bit).
+    oracle.build()
+    lib = oracle.lib()
+    host = np.zeros(backing.numel() * backing.element_size(), dtype=np.uint8)
+    base = backing.data_ptr()
+    spans = plane.spans()
+    for s, (_, span_base, pitch, nbytes) in enumerate(spans):
+        start = span_base - base
+        for b in source:
+            host[start + b * pitch:start + b * pitch + nbytes] = oracle.fill_span(0, s, b, nbytes)
+    span_base = np.array([host.ctypes.data + (sp[1] - base) for sp in spans], dtype=np.uint64)
+    span_pitch = np.array([sp[2] for sp in spans], dtype=np.int64)
+    span_off = np.array([sp[0] for sp in spans], dtype=np.int64)
+    span_len = np.array([sp[3] for sp in spans], dtype=np.int64)
+    src_ids, dst_ids = np.array(source, dtype=np.int64), np.array(target, dtype=np.int64)
+    records = np.zeros(total, dtype=np.uint8)
+    crcs = np.zeros(session, dtype=np.uint32)
+    addresses = np.array([records.ctypes.data + i * size for i in range(session)], dtype=np.uint64)
+
+    def cpu_round_trip(threads):
+        lib.oracle_copy_threads(len(spans), span_base.ctypes.data, span_pitch.ctypes.data, span_off.ctypes.data,
+                                span_len.ctypes.data, src_ids.ctypes.data, None, session, records.ctypes.data,
+                                size, threads)
+        lib.oracle_digest_records(records.ctypes.data, size, size, session, crcs.ctypes.data, None, threads)
+        lib.oracle_copy_threads(len(spans), span_base.ctypes.data, span_pitch.ctypes.data, span_off.ctypes.data,
+                                span_len.ctypes.data, dst_ids.ctypes.data, addresses.ctypes.data, session, None,
+                                size, threads)
+
+    cpu_round_trip(1)                                   # first touch of the target pages, untimed
+    threads_max = max(1, min(16, os.cpu_count() or 1))
+    cpu = {}
+    for threads in sorted({1, threads_max}):
+        times = []
+        for _ in range(3):
+            t0 = time.perf_counter()
+            cpu_round_trip(threads)
+            times.append(time.perf_counter() - t0)
+        cpu[threads] = min(times)
+    cpu_exact = np.array_equal(oracle.gather([(int(span_base[i]), int(span_pitch[i]), int(span_off[i]),
+                                               int(span_len[i])) for i in range(len(spans))], target, size),
+                               records.reshape(session, size))
+
+    # GPU leg: save into pinned records, then a verified restore that must match the CPU's CRC32Cs.
+    staged = plane.pool.reserve(total)
+    targets = [(staged, i * size) for i in range(session)]
+    expected = [int(c) for c in crcs]
+    gpu = []
+    for _ in range(4):
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        plane.save_gather(source, targets, tokens)
+        plane.load_scatter_verified(target, targets, expected)
+        torch.cuda.synchronize()
+        gpu.append(time.perf_counter() - t0)
+    gpu_ms = statistics.median(gpu[1:]) * 1e3
+    records_equal = np.array_equal(np.frombuffer(ctypes.string_at(staged.pointer, total), dtype=np.uint8), records)
+    exact = same_blocks(torch, caches, source, target)
+    staged.close()
+    plane.close()
+    return {"metric": "CPU reference round trip at the Qwen3-1.7B shape (gather, CRC32C, scatter, compare)",
+            "workload": "cpu-roundtrip", "value": round(2 * total / (gpu_ms * 1e6), 2),
+            "unit": "GB/s (GPU: save + CRC-verified restore, save and restore bytes)", "record_bytes": size,
+            "session_blocks": session, "gpu_ms": round(gpu_ms, 2),
+            "cpu_baseline": {"value": round(2 * total / cpu[threads_max] / 1e9, 3), "unit": "GB/s",
+                             "cores": threads_max, "kind": "port",
+                             "single_thread_gbps": round(2 * total / cpu[1] / 1e9, 3),
+                             "ms": {str(t): round(v * 1e3, 2) for t, v in cpu.items()},
+                             "sample": f"the whole case: {session} blocks x {size} B gathered, CRC32C'd and "
+                                       "scattered into a fresh table, best of 3"},
+            # load_scatter_verified raises before any KV write unless every GPU CRC32C equals the CPU's.
+            "parity": {"cpu_round_trip_exact": bool(cpu_exact), "gpu_records_equal_cpu_records": bool(records_equal),
+                       "gpu_crc32c_equal_cpu": True, "gpu_restore_exact": exact},
+            "layout": args.layout}
+
+
 # ---------------------------------------------------------------- multi-turn host-tier saves
 
 def run_turns(args):
@@ -694,8 +798,8 @@ def main():
     parser.add_argument("--steps", type=int, default=10)
     parser.add_argument("--warmup", type=int, default=3)
     parser.add_argument("--layout", choices=("kv_split", "vllm"), default="kv_split")
-    parser.add_argument("--workload", choices=("save-restore", "disk-fork", "rotating-fp8", "turns", "kernels"),
-                        default="save-restore")
+    parser.add_argument("--workload", choices=("save-restore", "disk-fork", "rotating-fp8", "turns", "cpu-roundtrip",
+                                               "kernels"), default="save-restore")
     parser.add_argument("--reps", type=int, default=5, help="kernels: timed repetitions per kernel")
     parser.add_argument("--hash-depth", type=int, default=2,
                         help="save-restore: steps a save's digests may trail before they are collected")
@@ -716,7 +820,7 @@ def main():
     import torch
     torch.cuda.set_device(0)
     runner = {"save-restore": run_save_restore, "disk-fork": run_disk_fork, "rotating-fp8": run_rotating,
-              "turns": run_turns, "kernels": run_kernels}
+              "turns": run_turns, "cpu-roundtrip": run_cpu_roundtrip, "kernels": run_kernels}
     print(json.dumps(runner[args.workload](args)), flush=True)
 
 
