@@ -112,13 +112,28 @@ __global__ __launch_bounds__(kGatherThreads) void gather_kernel(
 }
 
 // Scatter from packed records in device memory (HBM to HBM, the verified
-// restore's last step): the gather's inverse, with its shape.
+// restore's last step): the gather's inverse, with its shape.  Workgroups are
+// dealt to the 8 XCDs round robin (workgroup i runs on XCD i % 8); here each
+// XCD takes one contiguous range of jobs, so a record's spans are read through
+// one XCD's L2.  That measured 5.66 TB/s against 5.26 with the jobs dealt
+// round robin; the gather, whose writes are the contiguous side, gained nothing.
+constexpr int kXcds = 8;
+
 __global__ __launch_bounds__(kScatterThreads) void scatter_kernel(
     const char* __restrict__ records, int64_t record_pitch, const int64_t* __restrict__ blocks, int64_t n_blocks,
     const int64_t* __restrict__ offs, const int64_t* __restrict__ bases, const int64_t* __restrict__ pitches,
     const int64_t* __restrict__ words, int64_t n_spans) {
     const int64_t jobs = n_blocks * n_spans;
-    for (int64_t job = blockIdx.x; job < jobs; job += gridDim.x) {
+    const int64_t grid = gridDim.x;
+    int64_t first = blockIdx.x, end = jobs, stride = grid;
+    if (grid >= kXcds) {
+        const int64_t per_xcd = (jobs + kXcds - 1) / kXcds;
+        const int64_t xcd = blockIdx.x % kXcds;
+        first = xcd * per_xcd + blockIdx.x / kXcds;
+        end = (xcd + 1) * per_xcd < jobs ? (xcd + 1) * per_xcd : jobs;
+        stride = (grid - xcd + kXcds - 1) / kXcds;  // workgroups on this XCD
+    }
+    for (int64_t job = first; job < end; job += stride) {
         const int64_t b = job / n_spans, s = job - b * n_spans;
         const char* src = records + b * record_pitch + offs[s];
         char* dst = reinterpret_cast<char*>(bases[s] + blocks[b] * pitches[s]);
