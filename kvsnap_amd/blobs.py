@@ -6,7 +6,9 @@ length, CRC32C of the payload, 8 zero bytes), then the payload.  A blob's file
 name is its payload's SHA-256 in lowercase hex plus ``.blob``; files are
 written to a temporary name, optionally fdatasync'ed, and renamed.
 
-``read_prepared_into`` is the restore's disk stage (reference
+``save`` is the save side: GPU gather, GPU ids and CRCs, blob writes, and
+delta saves of a growing session.  ``read_prepared_into`` is the restore's
+disk stage (reference
 ``kvsnap/store/store.py:686-723``): block ``first_block + i`` is pread into
 ``address + i * block_bytes`` of a pinned buffer, by ``workers`` threads,
 under a shared lock on ``<root>/.blob.lock``.  Every block's CRC32C is checked
@@ -117,6 +119,52 @@ class BlobDirectory:
         return [dict(blob_id=blob_id, offset=0, length=data[1] if isinstance(data, tuple) else len(data),
                      first_block=index, nblocks=1, crc32c=crc)
                 for index, (data, (blob_id, crc)) in enumerate(zip(blocks, digests))]
+
+    def save(self, plane, block_ids, num_kv_tokens, *, previous=None, durable=False, workers=8, fenced=None,
+             chunk_bytes=64 << 20):
+        """Save a session's blocks as blob files; returns the snapshot ``{block_ids, num_kv_tokens, segments}``.
+
+        The blocks are gathered on the GPU into pinned staging, hashed there
+        (SHA-256 id and CRC32C per block) and written under their ids, with
+        repeated ids written once.  With ``previous`` (a snapshot of this
+        session saved here, or restored into the same block ids), the
+        unchanged prefix (:func:`kvsnap_amd.host_tier.unchanged_prefix`)
+        keeps its segments, whose blobs already exist, and only the rest is
+        gathered, copied, hashed and written: the reference's blob writer
+        rehashes every block (``store.py:616-628``).  The segments equal those
+        of a full save.  ``fenced.set()`` is called once the GPU blocks may be
+        freed, before the hashes and writes.  ``self.gathered_blocks`` counts
+        the blocks this call gathered.
+        """
+        from .host_tier import unchanged_prefix
+        block_size, size = plane.block_size, plane.block_bytes
+        block_ids = list(block_ids)
+        if len(block_ids) != (num_kv_tokens + block_size - 1) // block_size:
+            raise ValueError("block count does not cover computed tokens")
+        keep = unchanged_prefix(block_ids, previous, block_size)
+        for index in range(keep):
+            if not self.path(previous["segments"][index]["blob_id"]).exists():
+                keep = index
+                break
+        segments = [dict(segment, first_block=i) for i, segment in enumerate(previous["segments"][:keep])] \
+            if keep else []
+        fresh = block_ids[keep:]
+        self.gathered_blocks = len(fresh)
+        self.written = 0
+        if not fresh:
+            if fenced is not None:
+                fenced.set()
+            return dict(block_ids=block_ids, num_kv_tokens=num_kv_tokens, segments=segments)
+        with plane.staging(len(fresh)) as staged:
+            digests = []
+            plane.save_gather(fresh, [(staged, i * size) for i in range(len(fresh))], num_kv_tokens - keep * block_size,
+                              chunk_bytes=chunk_bytes, digests=digests)
+            if fenced is not None:
+                fenced.set()
+            new = self.write_blocks([(staged.pointer + i * size, size) for i in range(len(fresh))],
+                                    digests[0].result(), durable=durable, workers=workers)
+        segments += [dict(segment, first_block=keep + segment["first_block"]) for segment in new]
+        return dict(block_ids=block_ids, num_kv_tokens=num_kv_tokens, segments=segments)
 
     def read_prepared_into(self, segments, address, block_bytes, *, first_block=0, workers=8, verify="host"):
         """pread blocks into packed pinned memory; with ``verify="host"`` CRC-check each one there."""

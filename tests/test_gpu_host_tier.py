@@ -147,3 +147,31 @@ def test_a_corrupted_held_block_is_refused_by_the_verified_restore(plane):
     byte.value ^= 0x10
     tier.restore(ids[4:], snapshot, verify=True)
     tier.release(snapshot)
+
+
+@pytest.mark.parametrize("verify", ["gpu", "host"])
+def test_disk_delta_save_equals_a_full_save_and_restores_byte_exact(plane, oracle_lib, tmp_path, verify):
+    from kvsnap_amd.blobs import BlobDirectory
+    ids = random.Random(21).sample(range(1, BLOCKS), 26)
+    delta, full = BlobDirectory(tmp_path / "delta"), BlobDirectory(tmp_path / "full")
+    first = delta.save(plane, ids[:20], 19 * BLOCK_SIZE + 6)
+    assert delta.gathered_blocks == 20 and delta.written == 20
+    refill(plane, ids[19:26], 55)
+    second = delta.save(plane, ids[:26], 25 * BLOCK_SIZE + 10, previous=first)
+    assert delta.gathered_blocks == 7 and delta.written == 7
+    reference = full.save(plane, ids[:26], 25 * BLOCK_SIZE + 10)
+    assert full.gathered_blocks == 26 and full.written == 26
+    assert second["segments"] == reference["segments"]
+    assert ids_crcs(second) == expected_segments(plane, oracle_lib, ids[:26], 25 * BLOCK_SIZE + 10)
+    # The delta snapshot restores from disk into other blocks, byte for byte.
+    others = [b for b in range(1, BLOCKS) if b not in ids]
+    targets = random.Random(22).sample(others, 26)
+    before = plane.backing.view(torch.int16).clone()
+    assert plane.load_from_disk(targets, delta, second["segments"], chunk_bytes=8 * plane.block_bytes,
+                                workers=2, verify=verify) == 4
+    torch.cuda.synchronize()
+    assert max(ids + targets) < plane.backing.shape[2]
+    expected = before.clone()
+    expected[:, :, targets] = before[:, :, ids]    # [layers, 2, blocks, N, H, D]
+    expected[:, :, targets[-1], 10:] = 0            # the snapshot's last block: slots past token 10 are zero
+    assert torch.equal(plane.backing.view(torch.int16), expected)
