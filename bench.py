@@ -31,7 +31,8 @@ Other workloads (one JSON line each, for the record; not the headline):
                               tokens a turn, each turn end saved into the host
                               tier in full (every block gathered and hashed, as
                               the reference rehashes every block) and by delta
-                              (only the blocks past the unchanged prefix)
+                              (only the blocks past the unchanged prefix), and
+                              by delta as blob files
     --workload cpu-roundtrip  the reference's CPU-runnable case (Qwen3-1.7B shape,
                               4096-block cache, 2048-token session): gather,
                               CRC32C, scatter, compare -- on the host cores
@@ -700,6 +701,7 @@ def run_turns(args):
     import torch
     from kvsnap_amd import synth
     from kvsnap_amd.dataplane import TorchBlockDataPlane
+    from kvsnap_amd.blobs import BlobDirectory
     from kvsnap_amd.host_tier import HostTier
 
     layers, num_blocks, block_size = 36, 16384, 16
@@ -715,7 +717,9 @@ def run_turns(args):
     del keep
     ids = random.Random(1).sample(range(1, num_blocks), final)
     full, delta = HostTier(plane, 2 * final * size), HostTier(plane, 2 * final * size)
-    prev_full = prev_delta = None
+    root = tempfile.mkdtemp(prefix="kvsnap-turns-", dir=args.disk_dir)
+    disk = BlobDirectory(root)
+    prev_full = prev_delta = prev_disk = None
     rows = []
     for turn in range(turns + 1):
         tokens = start_tokens + turn * turn_tokens
@@ -732,31 +736,40 @@ def run_turns(args):
         t1 = time.perf_counter()
         snap_delta = delta.save(ids[:count], tokens, previous=prev_delta, fenced=fence_delta)
         t2 = time.perf_counter()
-        if snap_full["segments"] != snap_delta["segments"]:
-            raise RuntimeError(f"turn {turn}: the delta save's segments differ from the full save's")
+        fence_disk = Stamp()
+        t3 = time.perf_counter()
+        snap_disk = disk.save(plane, ids[:count], tokens, previous=prev_disk, fenced=fence_disk)
+        t4 = time.perf_counter()
+        if not snap_full["segments"] == snap_delta["segments"] == snap_disk["segments"]:
+            raise RuntimeError(f"turn {turn}: the delta saves' segments differ from the full save's")
         rows.append(dict(turn=turn, tokens=tokens, blocks=count,
                          full_fenced_ms=round((fence_full.at - t0) * 1e3, 2), full_ms=round((t1 - t0) * 1e3, 2),
                          full_gathered=full.gathered_blocks,
                          delta_fenced_ms=round((fence_delta.at - t1) * 1e3, 2), delta_ms=round((t2 - t1) * 1e3, 2),
-                         delta_gathered=delta.gathered_blocks))
+                         delta_gathered=delta.gathered_blocks,
+                         disk_fenced_ms=round((fence_disk.at - t3) * 1e3, 2), disk_ms=round((t4 - t3) * 1e3, 2),
+                         disk_written=disk.written))
         log(f"turn {turn}: {tokens} tokens; full: fenced {rows[-1]['full_fenced_ms']} ms, adopted "
             f"{rows[-1]['full_ms']} ms; delta ({delta.gathered_blocks} blocks): fenced "
             f"{rows[-1]['delta_fenced_ms']} ms, adopted {rows[-1]['delta_ms']} ms")
         for tier, previous in ((full, prev_full), (delta, prev_delta)):
             if previous is not None:
                 tier.release(previous)
-        prev_full, prev_delta = snap_full, snap_delta
+        prev_full, prev_delta, prev_disk = snap_full, snap_delta, snap_disk
     cpu = None if args.no_cpu_baseline else turn_cpu_baseline(full, prev_full, size)
     later = rows[1:]
     median = lambda key: statistics.median(r[key] for r in later)
     for tier, previous in ((full, prev_full), (delta, prev_delta)):
         tier.release(previous)
     plane.close()
+    import shutil
+    shutil.rmtree(root, ignore_errors=True)
     return {"metric": "turn-end host-tier save of a growing Qwen3-8B session: ms until the GPU blocks are free "
                       "(D2H fenced), delta save",
             "workload": "turns", "value": median("delta_fenced_ms"), "unit": "ms", "higher_is_better": False,
             "full_fenced_ms": median("full_fenced_ms"), "delta_adopted_ms": median("delta_ms"),
-            "full_adopted_ms": median("full_ms"),
+            "full_adopted_ms": median("full_ms"), "disk_delta_fenced_ms": median("disk_fenced_ms"),
+            "disk_delta_written_ms": median("disk_ms"),
             "fence_speedup": round(median("full_fenced_ms") / median("delta_fenced_ms"), 2),
             "note": "adopted = digests computed on the GPU and the blocks held by content id; a record's "
                     "SHA-256 is one sequential chain, so both saves' adoption waits about one record's hash",
@@ -809,7 +822,7 @@ def main():
                         help="rotating-fp8: save mode of the plane (default direct)")
     parser.add_argument("--programs", type=int, default=None,
                         help="rotating-fp8: restore / direct-save workgroups (default 8)")
-    parser.add_argument("--disk-dir", default=None, help="disk-fork: where the blob files go")
+    parser.add_argument("--disk-dir", default=None, help="disk-fork, turns: where the blob files go")
     parser.add_argument("--cpu-seconds", type=float, default=20.0)
     parser.add_argument("--no-cpu-baseline", action="store_true")
     args = parser.parse_args()
