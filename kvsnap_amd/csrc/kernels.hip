@@ -616,7 +616,7 @@ __device__ __forceinline__ void sha_rounds_pair(uint32_t x[4], const u32x4 (*slo
 }
 
 constexpr int kShaThreads = 192;  // waves 0-1: rounds (32 records each); wave 2: message schedule (64 records)
-constexpr int kShaStep = 2;  // blocks per barrier; the producer fills one half while the rounds read the other
+constexpr int kShaStep = 4;  // blocks per barrier; the producer fills one half while the rounds read the other
 
 // The producer's step for block `blk`: expand the words loaded for it, then
 // start the loads of block blk + kShaStep into the same registers.  Each of
@@ -653,9 +653,9 @@ __global__ __launch_bounds__(kShaThreads) void sha256_kernel(const uint8_t* __re
     const uint64_t steps = (nblocks + kShaStep - 1) / kShaStep;
     uint32_t raw[kShaStep][16];
     if (producer) {
-        if (lane < 2 * kShaStep * kShaBlockQuads) {
-            const int slot = lane / kShaBlockQuads;
-            sched[slot / kShaStep][slot % kShaStep][lane % kShaBlockQuads][64] = u32x4{1u, 1u, 1u, 1u};
+        for (int i = lane; i < 2 * kShaStep * kShaBlockQuads; i += 64) {
+            const int slot = i / kShaBlockQuads;
+            sched[slot / kShaStep][slot % kShaStep][i % kShaBlockQuads][64] = u32x4{1u, 1u, 1u, 1u};
         }
 #pragma unroll
         for (int i = 0; i < kShaStep; ++i)
