@@ -430,6 +430,56 @@ def test_qwen3_8b_8k_session_at_full_size(planes, oracle_lib):
     staged.close()
 
 
+def test_an_early_reported_restore_is_complete_for_the_engine_stream(planes):
+    """The connector's protocol (reference vllm.py:454-466, 663-679): a loader thread runs the restore while the
+    engine polls its progress; at most 128 MiB left, the load is reported and the next forward waits on the last
+    launch's event (wait_on_engine_stream).  Work on the engine stream after that wait sees every restored byte."""
+    import threading
+    import time
+    from kvsnap_amd.ordering import EARLY_REPORT_BYTES, early_report
+    caches, backing = synth.make_caches(36, 1100, layout="kv_split")
+    size = 36 * 65536
+    plane = planes(caches, capacity=512 * size + (64 << 20))
+    keep = synth.fill(plane, 17)
+    torch.cuda.synchronize()
+    del keep
+    saved, restored = synth.block_tables(1100, 512)
+    assert max(saved + restored) < 1100
+    staged = plane.pool.reserve(512 * size)
+    sources = [(staged, i * size) for i in range(512)]
+    plane.save_gather(saved, sources, 512 * BLOCK_SIZE)
+    dst = torch.tensor(restored, device="cuda")
+    src = torch.tensor(saved, device="cuda")
+    for view in caches.values():                # [2, blocks, N, H, D]
+        view[:, dst] = 0
+    torch.cuda.synchronize()
+    progress, failure = [], []
+
+    def loader():
+        try:
+            plane.load_scatter(restored, sources, progress=progress)
+        except BaseException as exc:
+            failure.append(exc)
+
+    thread = threading.Thread(target=loader)
+    thread.start()
+    report, deadline = None, time.monotonic() + 30
+    while report is None and time.monotonic() < deadline and not failure:
+        report = early_report(list(progress))
+        time.sleep(0.0002)
+    assert report is not None and not failure
+    left, last = report
+    assert left <= EARLY_REPORT_BYTES
+    plane.wait_on_engine_stream(last)
+    # The next "forward": reads of the restored blocks, queued on the engine stream.
+    seen = [view[:, dst].clone() for view in caches.values()]
+    torch.cuda.current_stream().synchronize()
+    thread.join()
+    for view, got in zip(caches.values(), seen):
+        assert torch.equal(got.view(torch.int16), view[:, src].view(torch.int16))
+    staged.close()
+
+
 @pytest.mark.parametrize("seed", range(6))
 def test_copy_kernels_on_random_span_tables_including_8_byte_alignment(hip_library, oracle_lib, seed):
     """Random geometries: odd word counts, pitches that are odd multiples of 8 bytes, bases offset by 8,
