@@ -40,7 +40,9 @@ Other workloads (one JSON line each, for the record; not the headline):
                               and on the GPU on the same bytes, the GPU
                               restore checked against the CPU's CRC32Cs
     --workload kernels        each kernel alone plus a plain copy of known size
-                              (the driver for rocprofv3 counter runs)
+                              (the driver for rocprofv3 counter runs);
+                              --kv-heads 4/2/1 gives one tensor-parallel rank's
+                              shard at TP = 2/4/8 (4-16 KiB spans)
 """
 from __future__ import annotations
 
@@ -81,15 +83,20 @@ def log(*args):
     print(*args, file=sys.stderr, flush=True)
 
 
-def median_ms(torch, stream, fn, reps=5):
+def median_ms(torch, stream, fn, reps=5, batch=1):
+    """Median over ``reps`` of the time per call of ``fn``.  With ``batch`` > 1 a call is queued first and the
+    events bracket ``batch`` more, so the GPU never waits for the host to launch (short kernels)."""
     times = []
     for _ in range(reps):
         start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        if batch > 1:
+            fn()
         start.record(stream)
-        fn()
+        for _ in range(batch):
+            fn()
         end.record(stream)
         end.synchronize()
-        times.append(start.elapsed_time(end))
+        times.append(start.elapsed_time(end) / batch)
     return statistics.median(times)
 
 
@@ -281,9 +288,10 @@ def run_save_restore(args):
     tables = plane._load_tables()
     src_ids = torch.tensor(source, dtype=torch.int64, device="cuda")
     dst_ids = torch.tensor(target, dtype=torch.int64, device="cuda")
-    gather_blocks(src_ids, *tables, records.data_ptr(), size)
+    gather_blocks(src_ids, *tables, records.data_ptr(), size, min_span_bytes=plane.min_span_bytes)
     scatter_ms = median_ms(torch, torch.cuda.current_stream(),
-                           lambda: scatter_blocks(records.data_ptr(), size, dst_ids, *tables), reps=5)
+                           lambda: scatter_blocks(records.data_ptr(), size, dst_ids, *tables,
+                                                  min_span_bytes=plane.min_span_bytes), reps=5)
     del records
     scatter_achieved = 2 * total / (scatter_ms * 1e6)
     cpu = None if args.no_cpu_baseline else cpu_baseline(layers, 65536, args.cpu_seconds)
@@ -551,8 +559,9 @@ def run_kernels(args):
 
     layers, num_blocks, block_size, tokens = 36, 16384, 16, 8192
     session = tokens // block_size
-    caches, backing = synth.make_caches(layers, num_blocks, block_size=block_size, layout=args.layout)
-    plane = TorchBlockDataPlane(caches, block_size, session * layers * 65536 + (64 << 20))
+    caches, backing = synth.make_caches(layers, num_blocks, block_size=block_size, heads=args.kv_heads,
+                                        layout=args.layout)
+    plane = TorchBlockDataPlane(caches, block_size, session * layers * 8192 * args.kv_heads + (64 << 20))
     plane.warm_up()
     keep = synth.fill(plane, 0)
     torch.cuda.synchronize()
@@ -573,28 +582,33 @@ def run_kernels(args):
     work_bytes = int(lib.kvsnap_crc32c_workspace_bytes(size, session))
     work = torch.empty(work_bytes, dtype=torch.uint8, device="cuda")
     sha = torch.empty((session, 32), dtype=torch.uint8, device="cuda")
+    hint = plane.min_span_bytes
     runs = {
         "plain_copy": (lambda: other.copy_(stage), 2 * total, args.reps),
-        "gather_kernel": (lambda: gather_blocks(ids, *tables, stage.data_ptr(), size), 2 * total, args.reps),
+        "gather_kernel": (lambda: gather_blocks(ids, *tables, stage.data_ptr(), size, min_span_bytes=hint),
+                          2 * total, args.reps),
         "crc_stripes_kernel": (lambda: _check(lib, lib.kvsnap_crc32c_records(
             stage.data_ptr(), size, size, session, 0, crc.data_ptr(), work.data_ptr(), work_bytes,
             stream.cuda_stream)), total, args.reps),
-        "restore_kernel": (lambda: copy_host_blocks(pinned, dst, *tables), 2 * total, args.reps),
+        "restore_kernel": (lambda: copy_host_blocks(pinned, dst, *tables, min_span_bytes=hint), 2 * total,
+                           args.reps),
         # The verified restore's scatter: records in device staging, one workgroup per (block, span).
-        "scatter_kernel": (lambda: scatter_blocks(stage.data_ptr(), size, dst, *tables), 2 * total, args.reps),
+        "scatter_kernel": (lambda: scatter_blocks(stage.data_ptr(), size, dst, *tables, min_span_bytes=hint),
+                           2 * total, args.reps),
         "sha256_kernel": (lambda: _check(lib, lib.kvsnap_sha256_records(
             stage.data_ptr(), size, size, session, sha.data_ptr(), stream.cuda_stream)), total, 1),
     }
     out = {}
     for name, (fn, algorithmic, reps) in runs.items():
         fn()
-        ms = median_ms(torch, stream, fn, reps=reps)
+        ms = median_ms(torch, stream, fn, reps=reps, batch=1 if name == "sha256_kernel" else 4)
         out[name] = {"ms": round(ms, 4), "algorithmic_bytes": algorithmic,
                      "gbps": round(algorithmic / ms / 1e6, 1)}
     out["sha256_kernel"]["issue_roofline"] = sha_issue_bound(size, session, out["sha256_kernel"]["ms"])
     staged.close()
     plane.close()
-    return {"workload": "kernels", "snapshot_bytes": total, "layout": args.layout, "kernels": out,
+    return {"workload": "kernels", "snapshot_bytes": total, "layout": args.layout, "kv_heads": args.kv_heads,
+            "span_bytes": sorted({s[3] for s in plane.spans()}), "kernels": out,
             "note": "restore_kernel reads pinned host records (link) and writes HBM; bytes counted both ways"}
 
 
@@ -814,6 +828,8 @@ def main():
     parser.add_argument("--workload", choices=("save-restore", "disk-fork", "rotating-fp8", "turns", "cpu-roundtrip",
                                                "kernels"), default="save-restore")
     parser.add_argument("--reps", type=int, default=5, help="kernels: timed repetitions per kernel")
+    parser.add_argument("--kv-heads", type=int, default=8, choices=(1, 2, 4, 8),
+                        help="kernels: KV heads in the cache, 8 / TP for one tensor-parallel rank's shard")
     parser.add_argument("--hash-depth", type=int, default=2,
                         help="save-restore: steps a save's digests may trail before they are collected")
     parser.add_argument("--rounds", type=int, default=4, help="rotating-fp8: rounds over the four sessions")

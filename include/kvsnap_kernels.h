@@ -14,6 +14,12 @@
  * span_offsets[s] of the block's packed record.  One span per layer for the
  * reference's [blocks, H, N, C] caches (in sorted layer-name order), two per
  * layer (K, then V) for [2, blocks, N, H, C] caches.
+ *
+ * Copy launches take `min_span_bytes`, the length of the shortest span (0 if
+ * unknown): a launch-shape hint that never changes what is copied.  Short
+ * spans (a tensor-parallel rank's shard, fp8 caches) are then copied several
+ * to a workgroup.  `programs` caps the grid (<= 0: as many workgroups as the
+ * jobs need).
  */
 #ifndef KVSNAP_KERNELS_H
 #define KVSNAP_KERNELS_H
@@ -25,25 +31,37 @@
 extern "C" {
 #endif
 
-/* Always 1. */
+/* Always 2 (2 added min_span_bytes to the copy launches). */
 int kvsnap_kernels_abi_version(void);
 
 /* Restore: for every (block i, span s), copy span_words[s] words from
  * sources[i] + span_offsets[s] to span_bases[s] + blocks[i] * span_pitches[s].
- * `programs` workgroups (<= 0: one per job).  Replaces the Triton launch
- * copy_host_blocks(sources, blocks, layer_offsets, layer_bases,
- * layer_pitches, layer_words), kvsnap/connector/copy_kernel.py:43-49
- * (kernel :22-40), called from kvsnap/connector/dataplane.py:374. */
+ * Replaces the Triton launch copy_host_blocks(sources, blocks,
+ * layer_offsets, layer_bases, layer_pitches, layer_words),
+ * kvsnap/connector/copy_kernel.py:43-49 (kernel :22-40), called from
+ * kvsnap/connector/dataplane.py:374. */
 int kvsnap_restore_blocks(const int64_t* sources, const int64_t* blocks, int64_t n_blocks,
                           const int64_t* span_offsets, const int64_t* span_bases, const int64_t* span_pitches,
-                          const int64_t* span_words, int64_t n_spans, int programs, uintptr_t stream);
+                          const int64_t* span_words, int64_t n_spans, int64_t min_span_bytes, int programs,
+                          uintptr_t stream);
 
 /* Gather: block blocks[i]'s spans packed into records + i * record_pitch.
  * Replaces save_gather's torch.cat([raw.index_select(0, ids) ...], out=stage),
  * kvsnap/connector/dataplane.py:416-417. */
 int kvsnap_gather_blocks(const int64_t* blocks, int64_t n_blocks, const int64_t* span_offsets,
                          const int64_t* span_bases, const int64_t* span_pitches, const int64_t* span_words,
-                         int64_t n_spans, void* records, int64_t record_pitch, int programs, uintptr_t stream);
+                         int64_t n_spans, int64_t min_span_bytes, void* records, int64_t record_pitch, int programs,
+                         uintptr_t stream);
+
+/* Gather into per-block destinations: block blocks[i]'s spans written to
+ * dests[i] + span_offsets[s], typically pinned host records written in place
+ * over the host link (a save without a device staging buffer).  Replaces the
+ * same gather (kvsnap/connector/dataplane.py:416-417) followed by its D2H
+ * copies into per-block allocations (:418-427). */
+int kvsnap_gather_to_records(const int64_t* dests, const int64_t* blocks, int64_t n_blocks,
+                             const int64_t* span_offsets, const int64_t* span_bases, const int64_t* span_pitches,
+                             const int64_t* span_words, int64_t n_spans, int64_t min_span_bytes, int programs,
+                             uintptr_t stream);
 
 /* Scatter: the record at records + i * record_pitch, in device memory, into
  * block blocks[i]'s spans; the gather's inverse.  The last step of a restore
@@ -52,7 +70,8 @@ int kvsnap_gather_blocks(const int64_t* blocks, int64_t n_blocks, const int64_t*
  * device-resident sources, with an HBM-to-HBM grid shape. */
 int kvsnap_scatter_blocks(const void* records, int64_t record_pitch, const int64_t* blocks, int64_t n_blocks,
                           const int64_t* span_offsets, const int64_t* span_bases, const int64_t* span_pitches,
-                          const int64_t* span_words, int64_t n_spans, int programs, uintptr_t stream);
+                          const int64_t* span_words, int64_t n_spans, int64_t min_span_bytes, int programs,
+                          uintptr_t stream);
 
 /* Zero n byte ranges [base + offsets[i], + lengths[i]): the token slots past
  * the last computed token of a record.  Replaces the host memsets of

@@ -44,43 +44,74 @@ constexpr int kThreads = 256;   // CRC, zero and synthetic-fill workgroups: 4 wa
 
 // ----------------------------------------------------------------- copies
 
-// Copy nbytes (a multiple of 8; src and dst 8-byte aligned) with the whole
-// workgroup of kT lanes, kU dwordx4 loads in flight per lane.  The 16-byte
-// path covers everything when both ends are 16-byte aligned, which the host
-// tables normally guarantee; an 8-byte tail covers the rest.
-template <int kT, int kU>
-__device__ __forceinline__ void copy_span(const char* __restrict__ src, char* __restrict__ dst, int64_t nbytes) {
-    const int tid = threadIdx.x;
+// Copy nbytes (a multiple of 8; src and dst 8-byte aligned) with `lanes`
+// lanes of the workgroup (this one is `lane`), kU dwordx4 loads in flight per
+// lane.  The 16-byte path covers everything when both ends are 16-byte
+// aligned, which the host tables normally guarantee; an 8-byte tail covers
+// the rest.
+template <int kU>
+__device__ __forceinline__ void copy_span(const char* __restrict__ src, char* __restrict__ dst, int64_t nbytes,
+                                          int lane, int lanes) {
     int64_t done = 0;
     if (((reinterpret_cast<uintptr_t>(src) | reinterpret_cast<uintptr_t>(dst)) & 15) == 0) {
         const u32x4* s = reinterpret_cast<const u32x4*>(src);
         u32x4* d = reinterpret_cast<u32x4*>(dst);
         const int64_t nv = nbytes >> 4;
-        int64_t i = tid;
-        for (; i + (kU - 1) * kT < nv; i += kU * kT) {
+        int64_t i = lane;
+        for (; i + (kU - 1) * lanes < nv; i += kU * lanes) {
             u32x4 v[kU];
 #pragma unroll
-            for (int u = 0; u < kU; ++u) v[u] = __builtin_nontemporal_load(s + i + u * kT);
+            for (int u = 0; u < kU; ++u) v[u] = __builtin_nontemporal_load(s + i + u * lanes);
 #pragma unroll
-            for (int u = 0; u < kU; ++u) __builtin_nontemporal_store(v[u], d + i + u * kT);
+            for (int u = 0; u < kU; ++u) __builtin_nontemporal_store(v[u], d + i + u * lanes);
         }
-        for (; i < nv; i += kT) __builtin_nontemporal_store(__builtin_nontemporal_load(s + i), d + i);
+        // Fewer than kU vectors left for this lane: still every load before any store.
+        if (i < nv) {
+            u32x4 v[kU] = {};
+#pragma unroll
+            for (int u = 0; u < kU; ++u)
+                if (i + u * lanes < nv) v[u] = __builtin_nontemporal_load(s + i + u * lanes);
+#pragma unroll
+            for (int u = 0; u < kU; ++u)
+                if (i + u * lanes < nv) __builtin_nontemporal_store(v[u], d + i + u * lanes);
+        }
         done = nv << 4;
     }
     const uint64_t* s8 = reinterpret_cast<const uint64_t*>(src + done);
     uint64_t* d8 = reinterpret_cast<uint64_t*>(dst + done);
     const int64_t nw = (nbytes - done) >> 3;
-    for (int64_t i = tid; i < nw; i += kT) d8[i] = s8[i];
+    for (int64_t i = lane; i < nw; i += lanes) d8[i] = s8[i];
+}
+
+// Jobs are (block, span) pairs, job j = (block j / n_spans, span j % n_spans):
+// the reference kernel's order (copy_kernel.py:29-31), so a launch walks its
+// records front to back.  A workgroup copies kT >> lane_shift jobs at a time,
+// one per group of 2^lane_shift lanes.  The host picks lane_shift from the
+// shortest span: the whole workgroup for the 32-64 KiB spans of a full bf16
+// cache, down to one wave for the 4 KiB spans of a tensor-parallel shard, so
+// that a pass keeps about kT * kU loads in flight whatever the span length.
+// A group is at least one wave, so its job index (and the table reads that
+// follow from it) is wave-uniform.
+struct JobLanes {
+    int lane, lanes, group, per_pass;
+};
+
+template <int kT>
+__device__ __forceinline__ JobLanes job_lanes(int lane_shift) {
+    JobLanes j;
+    j.lanes = 1 << lane_shift;
+    j.per_pass = kT >> lane_shift;
+    j.group = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) >> lane_shift);
+    j.lane = static_cast<int>(threadIdx.x) & (j.lanes - 1);
+    return j;
 }
 
 // Restore: reads cross the host link, so a small persistent grid of 256-lane
 // workgroups with 8 loads in flight per lane keeps it full while leaving the
-// CUs to the engine.  Job j = (block j / n_spans, span j % n_spans): the
-// reference kernel's order (copy_kernel.py:29-31), so a launch walks its
-// records front to back.
+// CUs to the engine.
 constexpr int kRestoreThreads = 256, kRestoreUnroll = 8;
-// Gather: HBM to HBM, one 1024-lane workgroup per (block, span) job with 4
-// loads in flight per lane (64 KiB per pass), the fastest shape measured.
+// Gather: HBM to HBM, 1024-lane workgroups with 4 loads in flight per lane
+// (64 KiB per pass), the fastest shape measured.
 constexpr int kGatherThreads = 1024, kGatherUnroll = 4;
 // Scatter from device records: HBM to HBM like the gather, writes scattered.
 constexpr int kScatterThreads = 1024, kScatterUnroll = 4;
@@ -88,56 +119,65 @@ constexpr int kScatterThreads = 1024, kScatterUnroll = 4;
 __global__ __launch_bounds__(kRestoreThreads) void restore_kernel(
     const int64_t* __restrict__ sources, const int64_t* __restrict__ blocks, int64_t n_blocks,
     const int64_t* __restrict__ offs, const int64_t* __restrict__ bases, const int64_t* __restrict__ pitches,
-    const int64_t* __restrict__ words, int64_t n_spans) {
+    const int64_t* __restrict__ words, int64_t n_spans, int lane_shift) {
+    const JobLanes jl = job_lanes<kRestoreThreads>(lane_shift);
     const int64_t jobs = n_blocks * n_spans;
-    for (int64_t job = blockIdx.x; job < jobs; job += gridDim.x) {
+    for (int64_t job = static_cast<int64_t>(blockIdx.x) * jl.per_pass + jl.group; job < jobs;
+         job += static_cast<int64_t>(gridDim.x) * jl.per_pass) {
         const int64_t b = job / n_spans, s = job - b * n_spans;
         const char* src = reinterpret_cast<const char*>(sources[b] + offs[s]);
         char* dst = reinterpret_cast<char*>(bases[s] + blocks[b] * pitches[s]);
-        copy_span<kRestoreThreads, kRestoreUnroll>(src, dst, words[s] * 8);
+        copy_span<kRestoreUnroll>(src, dst, words[s] * 8, jl.lane, jl.lanes);
     }
 }
 
 __global__ __launch_bounds__(kGatherThreads) void gather_kernel(
     const int64_t* __restrict__ blocks, int64_t n_blocks, const int64_t* __restrict__ offs,
     const int64_t* __restrict__ bases, const int64_t* __restrict__ pitches, const int64_t* __restrict__ words,
-    int64_t n_spans, char* __restrict__ records, int64_t record_pitch) {
+    int64_t n_spans, char* __restrict__ records, int64_t record_pitch, int lane_shift) {
+    const JobLanes jl = job_lanes<kGatherThreads>(lane_shift);
     const int64_t jobs = n_blocks * n_spans;
-    for (int64_t job = blockIdx.x; job < jobs; job += gridDim.x) {
+    for (int64_t job = static_cast<int64_t>(blockIdx.x) * jl.per_pass + jl.group; job < jobs;
+         job += static_cast<int64_t>(gridDim.x) * jl.per_pass) {
         const int64_t b = job / n_spans, s = job - b * n_spans;
         const char* src = reinterpret_cast<const char*>(bases[s] + blocks[b] * pitches[s]);
         char* dst = records + b * record_pitch + offs[s];
-        copy_span<kGatherThreads, kGatherUnroll>(src, dst, words[s] * 8);
+        copy_span<kGatherUnroll>(src, dst, words[s] * 8, jl.lane, jl.lanes);
     }
 }
 
 // Scatter from packed records in device memory (HBM to HBM, the verified
 // restore's last step): the gather's inverse, with its shape.  Workgroups are
 // dealt to the 8 XCDs round robin (workgroup i runs on XCD i % 8); here each
-// XCD takes one contiguous range of jobs, so a record's spans are read through
-// one XCD's L2.  That measured 5.66 TB/s against 5.26 with the jobs dealt
-// round robin; the gather, whose writes are the contiguous side, gained nothing.
+// XCD takes one contiguous range of passes, so a record's spans are read
+// through one XCD's L2.  That measured 5.66 TB/s against 5.26 with the passes
+// dealt round robin; the gather, whose writes are the contiguous side, gained
+// nothing.
 constexpr int kXcds = 8;
 
 __global__ __launch_bounds__(kScatterThreads) void scatter_kernel(
     const char* __restrict__ records, int64_t record_pitch, const int64_t* __restrict__ blocks, int64_t n_blocks,
     const int64_t* __restrict__ offs, const int64_t* __restrict__ bases, const int64_t* __restrict__ pitches,
-    const int64_t* __restrict__ words, int64_t n_spans) {
+    const int64_t* __restrict__ words, int64_t n_spans, int lane_shift) {
+    const JobLanes jl = job_lanes<kScatterThreads>(lane_shift);
     const int64_t jobs = n_blocks * n_spans;
+    const int64_t passes = (jobs + jl.per_pass - 1) / jl.per_pass;
     const int64_t grid = gridDim.x;
-    int64_t first = blockIdx.x, end = jobs, stride = grid;
+    int64_t first = blockIdx.x, end = passes, stride = grid;
     if (grid >= kXcds) {
-        const int64_t per_xcd = (jobs + kXcds - 1) / kXcds;
+        const int64_t per_xcd = (passes + kXcds - 1) / kXcds;
         const int64_t xcd = blockIdx.x % kXcds;
         first = xcd * per_xcd + blockIdx.x / kXcds;
-        end = (xcd + 1) * per_xcd < jobs ? (xcd + 1) * per_xcd : jobs;
+        end = (xcd + 1) * per_xcd < passes ? (xcd + 1) * per_xcd : passes;
         stride = (grid - xcd + kXcds - 1) / kXcds;  // workgroups on this XCD
     }
-    for (int64_t job = first; job < end; job += stride) {
+    for (int64_t pass = first; pass < end; pass += stride) {
+        const int64_t job = pass * jl.per_pass + jl.group;
+        if (job >= jobs) continue;  // only in the last pass
         const int64_t b = job / n_spans, s = job - b * n_spans;
         const char* src = records + b * record_pitch + offs[s];
         char* dst = reinterpret_cast<char*>(bases[s] + blocks[b] * pitches[s]);
-        copy_span<kScatterThreads, kScatterUnroll>(src, dst, words[s] * 8);
+        copy_span<kScatterUnroll>(src, dst, words[s] * 8, jl.lane, jl.lanes);
     }
 }
 
@@ -147,13 +187,15 @@ __global__ __launch_bounds__(kScatterThreads) void scatter_kernel(
 __global__ __launch_bounds__(kRestoreThreads) void gather_to_kernel(
     const int64_t* __restrict__ dests, const int64_t* __restrict__ blocks, int64_t n_blocks,
     const int64_t* __restrict__ offs, const int64_t* __restrict__ bases, const int64_t* __restrict__ pitches,
-    const int64_t* __restrict__ words, int64_t n_spans) {
+    const int64_t* __restrict__ words, int64_t n_spans, int lane_shift) {
+    const JobLanes jl = job_lanes<kRestoreThreads>(lane_shift);
     const int64_t jobs = n_blocks * n_spans;
-    for (int64_t job = blockIdx.x; job < jobs; job += gridDim.x) {
+    for (int64_t job = static_cast<int64_t>(blockIdx.x) * jl.per_pass + jl.group; job < jobs;
+         job += static_cast<int64_t>(gridDim.x) * jl.per_pass) {
         const int64_t b = job / n_spans, s = job - b * n_spans;
         const char* src = reinterpret_cast<const char*>(bases[s] + blocks[b] * pitches[s]);
         char* dst = reinterpret_cast<char*>(dests[b] + offs[s]);
-        copy_span<kRestoreThreads, kRestoreUnroll>(src, dst, words[s] * 8);
+        copy_span<kRestoreUnroll>(src, dst, words[s] * 8, jl.lane, jl.lanes);
     }
 }
 
@@ -766,6 +808,27 @@ unsigned grid_for(int64_t jobs, int programs) {
     return static_cast<unsigned>(grid);
 }
 
+// A copy launch's shape: lanes per (block, span) job as a shift, and the grid.
+// A group of lanes keeps `unroll` 16-byte loads per lane in flight while its
+// span has at least twice that many vectors; shorter spans get fewer lanes,
+// never less than a wave.  min_span_bytes <= 0 (unknown) keeps whole
+// workgroups.  The shape never changes what is copied, only how fast.
+struct CopyShape {
+    int lane_shift;
+    unsigned grid;
+};
+
+CopyShape copy_shape(int threads, int unroll, int64_t jobs, int64_t min_span_bytes, int programs) {
+    int shift = 0;
+    while ((1 << (shift + 1)) <= threads) ++shift;
+    if (min_span_bytes > 0) {
+        const int64_t vectors = min_span_bytes / 16;
+        while (shift > 6 && (int64_t(1) << shift) * unroll > 2 * vectors) --shift;
+    }
+    const int64_t per_pass = threads >> shift;
+    return CopyShape{shift, grid_for((jobs + per_pass - 1) / per_pass, programs)};
+}
+
 struct CrcPlan {
     int64_t groups, stripes;
     uint64_t pad;
@@ -785,64 +848,78 @@ CrcPlan crc_plan(uint64_t record_bytes) {
 
 extern "C" {
 
-int kvsnap_kernels_abi_version() { return 1; }
+int kvsnap_kernels_abi_version() { return 2; }
 
 int kvsnap_restore_blocks(const int64_t* sources, const int64_t* blocks, int64_t n_blocks,
                           const int64_t* span_offsets, const int64_t* span_bases, const int64_t* span_pitches,
-                          const int64_t* span_words, int64_t n_spans, int programs, uintptr_t stream) {
+                          const int64_t* span_words, int64_t n_spans, int64_t min_span_bytes, int programs,
+                          uintptr_t stream) {
     return guard([&] {
         if (n_blocks < 0 || n_spans < 0) throw std::runtime_error("negative restore size");
         if (n_blocks == 0 || n_spans == 0) return;
         if (!sources || !blocks || !span_offsets || !span_bases || !span_pitches || !span_words)
             throw std::runtime_error("restore tables must be device pointers");
-        hipLaunchKernelGGL(restore_kernel, dim3(grid_for(n_blocks * n_spans, programs)), dim3(kRestoreThreads), 0,
+        const CopyShape shape = copy_shape(kRestoreThreads, kRestoreUnroll, n_blocks * n_spans, min_span_bytes,
+                                           programs);
+        hipLaunchKernelGGL(restore_kernel, dim3(shape.grid), dim3(kRestoreThreads), 0,
                            reinterpret_cast<hipStream_t>(stream), sources, blocks, n_blocks, span_offsets,
-                           span_bases, span_pitches, span_words, n_spans);
+                           span_bases, span_pitches, span_words, n_spans, shape.lane_shift);
         check_launch("restore");
     });
 }
 
 int kvsnap_scatter_blocks(const void* records, int64_t record_pitch, const int64_t* blocks, int64_t n_blocks,
                           const int64_t* span_offsets, const int64_t* span_bases, const int64_t* span_pitches,
-                          const int64_t* span_words, int64_t n_spans, int programs, uintptr_t stream) {
+                          const int64_t* span_words, int64_t n_spans, int64_t min_span_bytes, int programs,
+                          uintptr_t stream) {
     return guard([&] {
         if (n_blocks < 0 || n_spans < 0 || record_pitch < 0) throw std::runtime_error("negative scatter size");
         if (n_blocks == 0 || n_spans == 0) return;
         if (!records || !blocks || !span_offsets || !span_bases || !span_pitches || !span_words)
             throw std::runtime_error("scatter tables must be device pointers");
-        hipLaunchKernelGGL(scatter_kernel, dim3(grid_for(n_blocks * n_spans, programs)), dim3(kScatterThreads), 0,
+        const CopyShape shape = copy_shape(kScatterThreads, kScatterUnroll, n_blocks * n_spans, min_span_bytes,
+                                           programs);
+        hipLaunchKernelGGL(scatter_kernel, dim3(shape.grid), dim3(kScatterThreads), 0,
                            reinterpret_cast<hipStream_t>(stream), static_cast<const char*>(records), record_pitch,
-                           blocks, n_blocks, span_offsets, span_bases, span_pitches, span_words, n_spans);
+                           blocks, n_blocks, span_offsets, span_bases, span_pitches, span_words, n_spans,
+                           shape.lane_shift);
         check_launch("scatter");
     });
 }
 
 int kvsnap_gather_blocks(const int64_t* blocks, int64_t n_blocks, const int64_t* span_offsets,
                          const int64_t* span_bases, const int64_t* span_pitches, const int64_t* span_words,
-                         int64_t n_spans, void* records, int64_t record_pitch, int programs, uintptr_t stream) {
+                         int64_t n_spans, int64_t min_span_bytes, void* records, int64_t record_pitch, int programs,
+                         uintptr_t stream) {
     return guard([&] {
         if (n_blocks < 0 || n_spans < 0 || record_pitch < 0) throw std::runtime_error("negative gather size");
         if (n_blocks == 0 || n_spans == 0) return;
         if (!records || !blocks || !span_offsets || !span_bases || !span_pitches || !span_words)
             throw std::runtime_error("gather tables must be device pointers");
-        hipLaunchKernelGGL(gather_kernel, dim3(grid_for(n_blocks * n_spans, programs)), dim3(kGatherThreads), 0,
+        const CopyShape shape = copy_shape(kGatherThreads, kGatherUnroll, n_blocks * n_spans, min_span_bytes,
+                                           programs);
+        hipLaunchKernelGGL(gather_kernel, dim3(shape.grid), dim3(kGatherThreads), 0,
                            reinterpret_cast<hipStream_t>(stream), blocks, n_blocks, span_offsets, span_bases,
-                           span_pitches, span_words, n_spans, static_cast<char*>(records), record_pitch);
+                           span_pitches, span_words, n_spans, static_cast<char*>(records), record_pitch,
+                           shape.lane_shift);
         check_launch("gather");
     });
 }
 
 int kvsnap_gather_to_records(const int64_t* dests, const int64_t* blocks, int64_t n_blocks,
                              const int64_t* span_offsets, const int64_t* span_bases, const int64_t* span_pitches,
-                             const int64_t* span_words, int64_t n_spans, int programs, uintptr_t stream) {
+                             const int64_t* span_words, int64_t n_spans, int64_t min_span_bytes, int programs,
+                             uintptr_t stream) {
     return guard([&] {
         if (n_blocks < 0 || n_spans < 0) throw std::runtime_error("negative gather size");
         if (n_blocks == 0 || n_spans == 0) return;
         if (!dests || !blocks || !span_offsets || !span_bases || !span_pitches || !span_words)
             throw std::runtime_error("gather tables must be device pointers");
-        hipLaunchKernelGGL(gather_to_kernel, dim3(grid_for(n_blocks * n_spans, programs)), dim3(kRestoreThreads), 0,
+        const CopyShape shape = copy_shape(kRestoreThreads, kRestoreUnroll, n_blocks * n_spans, min_span_bytes,
+                                           programs);
+        hipLaunchKernelGGL(gather_to_kernel, dim3(shape.grid), dim3(kRestoreThreads), 0,
                            reinterpret_cast<hipStream_t>(stream), dests, blocks, n_blocks, span_offsets, span_bases,
-                           span_pitches, span_words, n_spans);
+                           span_pitches, span_words, n_spans, shape.lane_shift);
         check_launch("gather to records");
     });
 }

@@ -68,14 +68,15 @@ class HostPool:
         pass
 
 
-def emulated_restore(sources, blocks, offsets, bases, pitches, words, *, programs=None):
+def emulated_restore(sources, blocks, offsets, bases, pitches, words, *, programs=None, min_span_bytes=0):
     spans = list(zip(*(t.tolist() for t in (offsets, bases, pitches, words))))
     for source, block in zip(sources.tolist(), blocks.tolist()):
         for offset, base, pitch, count in spans:
             C.memmove(base + block * pitch, source + offset, count * 8)
 
 
-def emulated_gather(blocks, offsets, bases, pitches, words, records, record_pitch, *, programs=None):
+def emulated_gather(blocks, offsets, bases, pitches, words, records, record_pitch, *, programs=None,
+                    min_span_bytes=0):
     spans = list(zip(*(t.tolist() for t in (offsets, bases, pitches, words))))
     for i, block in enumerate(blocks.tolist()):
         for offset, base, pitch, count in spans:

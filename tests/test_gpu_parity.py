@@ -483,11 +483,14 @@ def test_an_early_reported_restore_is_complete_for_the_engine_stream(planes):
 @pytest.mark.parametrize("seed", range(6))
 def test_copy_kernels_on_random_span_tables_including_8_byte_alignment(hip_library, oracle_lib, seed):
     """Random geometries: odd word counts, pitches that are odd multiples of 8 bytes, bases offset by 8,
-    so the kernels' 8-byte path runs beside the 16-byte one; gather, restore, scatter and gather-to-records."""
+    so the kernels' 8-byte path runs beside the 16-byte one; gather, restore, scatter and gather-to-records.
+    The span-length hint only shapes the launches: unknown, right, far too short and far too long all give
+    the oracle's bytes."""
     rng = np.random.default_rng(100 + seed)
     blocks = int(rng.integers(4, 40))
     n_spans = int(rng.integers(1, 9))
-    words = [int(rng.integers(1, 700)) for _ in range(n_spans)]
+    words = [int(rng.integers(1, 3000 if s % 2 else 700)) for s in range(n_spans)]
+    hint = [0, 8 * min(words), 16, 1 << 20, 8 * min(words), 4096][seed]
     pitches = [w + int(rng.integers(0, 5)) for w in words]                     # 8-byte words
     shifts = [int(rng.integers(0, 2)) for _ in range(n_spans)]                 # 0 or 1 word of misalignment
     offsets = np.cumsum([0] + words[:-1]).tolist()
@@ -512,7 +515,7 @@ def test_copy_kernels_on_random_span_tables_including_8_byte_alignment(hip_libra
     # gather into a device buffer at an 8-byte (not 16) offset
     out = torch.zeros(count * record_words + 1, dtype=torch.int64, device="cuda")
     _check(lib, lib.kvsnap_gather_blocks(dev(ids).data_ptr(), count, offs.data_ptr(), bases.data_ptr(),
-                                         pitch_b.data_ptr(), words_t.data_ptr(), n_spans, out.data_ptr() + 8,
+                                         pitch_b.data_ptr(), words_t.data_ptr(), n_spans, hint, out.data_ptr() + 8,
                                          record_words * 8, 0, stream))
     torch.cuda.synchronize()
     got = out.cpu().numpy()[1:].view(np.uint8).reshape(count, -1)
@@ -521,8 +524,8 @@ def test_copy_kernels_on_random_span_tables_including_8_byte_alignment(hip_libra
     dests = torch.zeros(count * (record_words + 1), dtype=torch.int64, device="cuda")
     dest_ptrs = dev([dests.data_ptr() + 8 * i * (record_words + 1) for i in range(count)])
     _check(lib, lib.kvsnap_gather_to_records(dest_ptrs.data_ptr(), dev(ids).data_ptr(), count, offs.data_ptr(),
-                                             bases.data_ptr(), pitch_b.data_ptr(), words_t.data_ptr(), n_spans, 7,
-                                             stream))
+                                             bases.data_ptr(), pitch_b.data_ptr(), words_t.data_ptr(), n_spans,
+                                             hint, 7, stream))
     torch.cuda.synchronize()
     rows = dests.cpu().numpy().reshape(count, record_words + 1)[:, :record_words]
     assert np.array_equal(rows.view(np.uint8).reshape(count, -1), expected)
@@ -530,8 +533,8 @@ def test_copy_kernels_on_random_span_tables_including_8_byte_alignment(hip_libra
     targets = rng.choice(blocks, count, replace=False).tolist()
     sources = dev([out.data_ptr() + 8 + i * record_words * 8 for i in range(count)])
     _check(lib, lib.kvsnap_restore_blocks(sources.data_ptr(), dev(targets).data_ptr(), count, offs.data_ptr(),
-                                          bases.data_ptr(), pitch_b.data_ptr(), words_t.data_ptr(), n_spans, 5,
-                                          stream))
+                                          bases.data_ptr(), pitch_b.data_ptr(), words_t.data_ptr(), n_spans, hint,
+                                          5, stream))
     torch.cuda.synchronize()
     after = [s.cpu().numpy() for s in stores]
     oracle_lib.scatter(spans, targets, [expected[i].ctypes.data for i in range(count)])
@@ -541,7 +544,7 @@ def test_copy_kernels_on_random_span_tables_including_8_byte_alignment(hip_libra
     third = rng.choice(blocks, count, replace=False).tolist()
     _check(lib, lib.kvsnap_scatter_blocks(out.data_ptr() + 8, record_words * 8, dev(third).data_ptr(), count,
                                           offs.data_ptr(), bases.data_ptr(), pitch_b.data_ptr(), words_t.data_ptr(),
-                                          n_spans, 3, stream))
+                                          n_spans, hint, 3, stream))
     torch.cuda.synchronize()
     after = [s.cpu().numpy() for s in stores]
     oracle_lib.scatter(spans, third, [expected[i].ctypes.data for i in range(count)])

@@ -44,7 +44,7 @@ def test_library_exports_every_declared_symbol(header):
 def test_abi_versions_without_a_gpu():
     hip = C.CDLL(str(HIP_LIBRARY))
     assert hip.kvsnap_pool_abi_version() == 2
-    assert hip.kvsnap_kernels_abi_version() == 1
+    assert hip.kvsnap_kernels_abi_version() == 2
     io = C.CDLL(str(IO_LIBRARY))
     assert io.kvsnap_io_abi_version() == 1
 
