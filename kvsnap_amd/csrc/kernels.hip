@@ -342,28 +342,48 @@ __global__ __launch_bounds__(kThreads) void synth_decode_kernel(const int64_t* _
 // with virtual zero bytes) whose raw CRCs are computed independently and
 // combined by Horner's rule; crc32c = ~(shift(~prior, N) ^ R(record)).
 //
-// Inside a stripe, lane t of a 256-lane workgroup reads the 16-byte word at
-// t*16 of every 4 KiB group (fully coalesced; all of the stripe's words are
-// loaded before any is folded, so a lane has 16 loads in flight), folds them
-// with
-//   acc = shift(acc, 4096) ^ R16(word),
-// and finally contributes shift(acc, (255 - t) * 16); the workgroup's XOR of
-// those is the stripe's raw CRC.  Tables (in LDS):
-//   T[i][v]  = shift(v, 16 - i)            slicing-by-16 for R16: byte i of
-//                                          the word, 16 independent lookups,
-//   G[k][v]  = shift(v << 8k, 4096)        the per-group advance.
-// Per-lane constants M[t] = x^(8 * 16 * (255 - t)) mod P are applied with a
+// Inside a stripe, lane t of a 1024-lane workgroup reads the 16-byte word at
+// t*16 of every 16 KiB group (fully coalesced; a batch of 16 groups is loaded
+// before any is folded, so a lane has 16 loads in flight), folds them with
+//   acc = shift(acc, 16384) ^ R16(word),
+// and finally contributes shift(acc, (1023 - t) * 16); the workgroup's XOR of
+// those is the stripe's raw CRC.  R16 runs slicing-by-4 over the word's four
+// dwords, s = S0[b0] ^ S1[b1] ^ S2[b2] ^ S3[b3] of (s ^ dword), with
+//   S[i][v]  = shift(v, 4 - i)
+// and the per-group advance uses
+//   G[k][v]  = shift(v << 8k, 16384).
+// Per-lane constants M[t] = x^(8 * 16 * (1023 - t)) mod P are applied with a
 // bitwise GF(2) multiply.
+//
+// The lookups are the kernel's cost, and random 8-bit indices into one shared
+// 1 KiB table put several lanes of a wave on the same LDS bank (61 % of the
+// LDS cycles were bank conflicts with shared tables).  So every lane reads
+// its own copy of S: entry v of S[i] for lane t sits at byte
+//   4096 + (i / 2) * 65536 + v * 256 + (i % 2) * 128 + (t % 32) * 4,
+// i.e. in bank t % 32, and the 32 lanes that an LDS pass serves never share a
+// bank.  The address is one byte move (v into byte 1 of a per-lane constant;
+// the 4096 rides in the instruction's offset field).  The four copies fill
+// 128 KiB of the 160 KiB LDS, so a CU holds one workgroup; the 4 KiB of G
+// stay shared (4 of the 20 lookups per word) at the front of the LDS, where
+// each table's base also fits the offset field.
+// A stripe is 16-48 groups (256-768 KiB), chosen per record size to keep the
+// zero padding in front of the first stripe small (Qwen3-8B records: three
+// 768 KiB stripes, no padding) and the per-lane multiply rare.
 
 constexpr uint32_t kPoly = 0x82F63B78u;
-constexpr int kGroup = kThreads * 16;  // bytes per group
-constexpr int kStripeGroups = 16;      // groups per stripe: 64 KiB stripes
-constexpr int kCrcGrid = 2048;         // persistent workgroups
+constexpr int kCrcThreads = 1024;
+constexpr int kCrcGroup = kCrcThreads * 16;  // bytes per group: one 16-byte word per lane
+constexpr int kCrcBatch = 16;                // groups loaded before they are folded
+constexpr int kCrcMinGroups = 16, kCrcMaxGroups = 48;
+constexpr int kCrcGrid = 256;                // persistent, one workgroup per CU
+constexpr int kCrcAdvanceBytes = 4 * 1024;   // G, shared, at LDS byte 0
+constexpr int kCrcPrivateBytes = 2 * 65536;  // the lanes' copies of S, after G
 
-constexpr int kCrcAdvance = 256 * 16;            // G's offset in g_crc_tables
-constexpr int kCrcLaneShift = kCrcAdvance + 256 * 4; // M's offset
+// g_crc_tables: S[4][256], then G[4][256], then M[kCrcThreads].
+constexpr int kCrcAdvance = 4 * 256;
+constexpr int kCrcLaneShift = kCrcAdvance + 4 * 256;
 
-__device__ uint32_t g_crc_tables[kCrcLaneShift + kThreads];
+__device__ uint32_t g_crc_tables[kCrcLaneShift + kCrcThreads];
 
 __device__ __forceinline__ uint32_t gf_mul(uint32_t a, uint32_t b) {
     // a * b mod P in the reflected representation (bit 31 is x^0).
@@ -376,45 +396,104 @@ __device__ __forceinline__ uint32_t gf_mul(uint32_t a, uint32_t b) {
     return p;
 }
 
-__device__ __forceinline__ uint32_t slice4(const uint32_t (*t)[256], uint32_t x) {
-    return t[0][x & 0xFF] ^ t[1][(x >> 8) & 0xFF] ^ t[2][(x >> 16) & 0xFF] ^ t[3][x >> 24];
+__device__ __forceinline__ uint32_t xor3(uint32_t a, uint32_t b, uint32_t c) {
+    return __builtin_amdgcn_bitop3_b32(a, b, c, 0x96);
 }
 
-__device__ __forceinline__ uint32_t fold16(const uint32_t (*t)[256], u32x4 v) {
-    uint32_t s = 0;
-#pragma unroll
-    for (int k = 0; k < 4; ++k) s ^= t[k][(v.x >> (8 * k)) & 0xFF] ^ t[4 + k][(v.y >> (8 * k)) & 0xFF];
-#pragma unroll
-    for (int k = 0; k < 4; ++k) s ^= t[8 + k][(v.z >> (8 * k)) & 0xFF] ^ t[12 + k][(v.w >> (8 * k)) & 0xFF];
-    return s;
+__device__ __forceinline__ uint32_t lds_word(const uint32_t* lds, uint32_t byte) {
+    return *reinterpret_cast<const uint32_t*>(reinterpret_cast<const char*>(lds) + byte);
+}
+
+// The per-lane address constant: byte 0 = the lane's column in S[0] and S[2],
+// byte 1 = its column in S[1] and S[3], byte 2 = 1 (the second 64 KiB).
+__device__ __forceinline__ uint32_t crc_columns(uint32_t lane) {
+    const uint32_t col = (lane & 31u) * 4u;
+    return col | ((col + 128u) << 8) | (1u << 16);
+}
+
+// One dword through slicing-by-4 from x = state ^ dword.  v_perm_b32 picks
+// bytes of {S0 = x (bytes 4-7), S1 = cols (bytes 0-3)}, selector 12 giving
+// 0x00: the address of S[i][byte i of x] is byte i of x in byte 1 above the
+// lane's column, one instruction per lookup:
+//   S[0]: ((x & 0xFF) << 8) | col                    selector 0x0C0C0400
+//   S[1]: (x & 0xFF00) | (col + 128)                  selector 0x0C0C0501
+//   S[2]: 0x10000 | ((x >> 8) & 0xFF00) | col          selector 0x0C020600
+//   S[3]: 0x10000 | ((x >> 16) & 0xFF00) | (col + 128) selector 0x0C020701
+__device__ __forceinline__ uint32_t crc_dword(const uint32_t* lds, uint32_t cols, uint32_t x) {
+    const uint32_t* s = lds + kCrcAdvanceBytes / 4;
+    const uint32_t a = lds_word(s, __builtin_amdgcn_perm(x, cols, 0x0C0C0400u));
+    const uint32_t b = lds_word(s, __builtin_amdgcn_perm(x, cols, 0x0C0C0501u));
+    const uint32_t c = lds_word(s, __builtin_amdgcn_perm(x, cols, 0x0C020600u));
+    const uint32_t d = lds_word(s, __builtin_amdgcn_perm(x, cols, 0x0C020701u));
+    return xor3(a, b, c) ^ d;
+}
+
+__device__ __forceinline__ uint32_t crc_word(const uint32_t* lds, uint32_t cols, u32x4 v) {
+    uint32_t s = crc_dword(lds, cols, v.x);
+    s = crc_dword(lds, cols, s ^ v.y);
+    s = crc_dword(lds, cols, s ^ v.z);
+    return crc_dword(lds, cols, s ^ v.w);
+}
+
+__device__ __forceinline__ uint32_t crc_advance(const uint32_t* lds, uint32_t acc) {
+    return xor3(lds_word(lds, (acc & 0xFFu) << 2), lds_word(lds, 1024u + (((acc >> 8) & 0xFFu) << 2)),
+                lds_word(lds, 2048u + (((acc >> 16) & 0xFFu) << 2))) ^
+           lds_word(lds, 3072u + ((acc >> 24) << 2));
 }
 
 template <bool kAligned>
-__global__ __launch_bounds__(kThreads) void crc_stripes_kernel(const uint8_t* __restrict__ records, uint64_t pitch,
-                                                              int64_t n_records, int64_t stripes, int64_t groups,
-                                                              uint64_t pad, uint32_t* __restrict__ partial) {
-    __shared__ uint32_t t16[16][256];
-    __shared__ uint32_t tg[4][256];
-    __shared__ uint32_t red[kThreads / 64];
-    for (int i = threadIdx.x; i < 4096; i += kThreads) t16[i >> 8][i & 255] = g_crc_tables[i];
-    for (int i = threadIdx.x; i < 1024; i += kThreads) tg[i >> 8][i & 255] = g_crc_tables[kCrcAdvance + i];
+__global__ __launch_bounds__(kCrcThreads) void crc_stripes_kernel(const uint8_t* __restrict__ records, uint64_t pitch,
+                                                                 int64_t n_records, int64_t stripes, int groups,
+                                                                 uint64_t pad, uint32_t* __restrict__ partial) {
+    __shared__ uint32_t lds[(kCrcAdvanceBytes + kCrcPrivateBytes) / 4];
+    __shared__ uint32_t red[kCrcThreads / 64];
+    for (int i = threadIdx.x; i < kCrcAdvanceBytes / 4; i += kCrcThreads) lds[i] = g_crc_tables[kCrcAdvance + i];
+    for (int w = threadIdx.x; w < kCrcPrivateBytes / 4; w += kCrcThreads) {
+        // word w of S: 64 KiB half w >> 14, entry (w >> 6) & 255, column w & 63 (table 2 * half + column / 32)
+        const int table = ((w >> 14) << 1) | ((w >> 5) & 1);
+        lds[kCrcAdvanceBytes / 4 + w] = g_crc_tables[table * 256 + ((w >> 6) & 255)];
+    }
     const uint32_t lane_shift = g_crc_tables[kCrcLaneShift + threadIdx.x];
+    const uint32_t cols = crc_columns(threadIdx.x);
     __syncthreads();
     const int64_t jobs = n_records * stripes;
-    const int64_t stripe_bytes = groups * kGroup;
+    const int64_t stripe_bytes = static_cast<int64_t>(groups) * kCrcGroup;
     for (int64_t job = blockIdx.x; job < jobs; job += gridDim.x) {
         const int64_t r = job / stripes, j = job - r * stripes;
         const uint8_t* rec = records + r * pitch;
-        // groups is 1 or kStripeGroups; bytes before the record (front padding) are zero.
-        u32x4 v[kStripeGroups];
+        uint32_t acc = 0;
+        for (int g0 = 0; g0 < groups; g0 += kCrcBatch) {
+            const int n = groups - g0 < kCrcBatch ? groups - g0 : kCrcBatch;  // workgroup-uniform
+            const int64_t batch_at = j * stripe_bytes + static_cast<int64_t>(g0) * kCrcGroup - static_cast<int64_t>(pad);
+            if (kAligned && n == kCrcBatch && batch_at >= 0) {
+                // Sixteen whole groups of the record: no padding, no predicates.  The words' slicing chains
+                // are independent, so they interleave; the advance chain follows.
+                const u32x4* at = reinterpret_cast<const u32x4*>(rec + batch_at) + threadIdx.x;
+                u32x4 v[kCrcBatch];
 #pragma unroll
-        for (int g = 0; g < kStripeGroups; ++g) {
-            v[g] = u32x4{0u, 0u, 0u, 0u};
-            const int64_t at = j * stripe_bytes + g * kGroup + threadIdx.x * 16 - static_cast<int64_t>(pad);
-            if (g < groups) {
+                for (int g = 0; g < kCrcBatch; ++g) v[g] = __builtin_nontemporal_load(at + g * (kCrcGroup / 16));
+                // Keep all sixteen loads ahead of the first fold (the scheduler would otherwise wait on the first).
+                __builtin_amdgcn_sched_barrier(0);
+                uint32_t r[kCrcBatch];
+#pragma unroll
+                for (int g = 0; g < kCrcBatch; ++g) r[g] = crc_word(lds, cols, v[g]);
+#pragma unroll
+                for (int g = 0; g < kCrcBatch; ++g) acc = crc_advance(lds, acc) ^ r[g];
+                continue;
+            }
+            u32x4 v[kCrcBatch];
+#pragma unroll
+            for (int g = 0; g < kCrcBatch; ++g) {
+                v[g] = u32x4{0u, 0u, 0u, 0u};
+                // Record-relative offsets; bytes before the record (front padding) are zero.
+                const int64_t group_at = j * stripe_bytes + static_cast<int64_t>(g0 + g) * kCrcGroup -
+                                         static_cast<int64_t>(pad);  // workgroup-uniform
+                const int64_t at = group_at + threadIdx.x * 16;
+                if (g >= n || group_at + kCrcGroup <= 0) continue;  // past the stripe, or all padding
                 if (kAligned) {
                     // The padding is a multiple of 16 here, so a word is all padding or all record.
-                    if (at >= 0) v[g] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(rec + at));
+                    if (group_at >= 0 || at >= 0)
+                        v[g] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(rec + at));
                 } else {
                     uint32_t w[4] = {0, 0, 0, 0};
                     for (int k = 0; k < 16; ++k)
@@ -422,17 +501,21 @@ __global__ __launch_bounds__(kThreads) void crc_stripes_kernel(const uint8_t* __
                     v[g] = u32x4{w[0], w[1], w[2], w[3]};
                 }
             }
-        }
-        uint32_t acc = 0;
 #pragma unroll
-        for (int g = 0; g < kStripeGroups; ++g)
-            if (g < groups) acc = slice4(tg, acc) ^ fold16(t16, v[g]);
+            for (int g = 0; g < kCrcBatch; ++g)
+                if (g < n) acc = crc_advance(lds, acc) ^ crc_word(lds, cols, v[g]);
+        }
         uint32_t x = gf_mul(lane_shift, acc);
 #pragma unroll
         for (int o = 32; o > 0; o >>= 1) x ^= __shfl_xor(x, o);
         if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = x;
         __syncthreads();
-        if (threadIdx.x == 0) partial[job] = red[0] ^ red[1] ^ red[2] ^ red[3];
+        if (threadIdx.x == 0) {
+            uint32_t sum = 0;
+#pragma unroll
+            for (int w = 0; w < kCrcThreads / 64; ++w) sum ^= red[w];
+            partial[job] = sum;
+        }
         __syncthreads();
     }
 }
@@ -476,9 +559,6 @@ __constant__ uint32_t kSha[64] = {
 };
 
 __device__ __forceinline__ uint32_t rotr(uint32_t x, int n) { return (x >> n) | (x << (32 - n)); }
-__device__ __forceinline__ uint32_t xor3(uint32_t a, uint32_t b, uint32_t c) {
-    return __builtin_amdgcn_bitop3_b32(a, b, c, 0x96);
-}
 __device__ __forceinline__ uint32_t bswap(uint32_t x) { return __builtin_bswap32(x); }
 
 constexpr int kShaBlockQuads = 16;  // 64 schedule words per block, read 4 at a time
@@ -772,15 +852,16 @@ void ensure_crc_tables() {
         throw std::runtime_error("no current HIP device for the CRC32C tables");
     std::lock_guard<std::mutex> lock(g_table_mutex);
     if (g_tables_ready[device]) return;
-    static uint32_t tables[kCrcLaneShift + kThreads];
-    for (uint32_t i = 0; i < 16; ++i) {
-        const uint32_t m = host_xpow8n(16 - i);
+    static uint32_t tables[kCrcLaneShift + kCrcThreads];
+    for (uint32_t i = 0; i < 4; ++i) {
+        const uint32_t m = host_xpow8n(4 - i);
         for (uint32_t v = 0; v < 256; ++v) tables[256 * i + v] = host_gf_mul(m, v);
     }
-    const uint32_t group_shift = host_xpow8n(kGroup);
+    const uint32_t group_shift = host_xpow8n(kCrcGroup);
     for (uint32_t k = 0; k < 4; ++k)
         for (uint32_t v = 0; v < 256; ++v) tables[kCrcAdvance + 256 * k + v] = host_gf_mul(group_shift, v << (8 * k));
-    for (uint32_t t = 0; t < kThreads; ++t) tables[kCrcLaneShift + t] = host_xpow8n(16ull * (kThreads - 1 - t));
+    for (uint32_t t = 0; t < kCrcThreads; ++t)
+        tables[kCrcLaneShift + t] = host_xpow8n(16ull * (kCrcThreads - 1 - t));
     hipError_t rc = hipMemcpyToSymbol(HIP_SYMBOL(g_crc_tables), tables, sizeof tables, 0, hipMemcpyHostToDevice);
     if (rc != hipSuccess) throw std::runtime_error(std::string("CRC32C table upload: ") + hipGetErrorString(rc));
     g_tables_ready[device] = true;
@@ -830,16 +911,31 @@ CopyShape copy_shape(int threads, int unroll, int64_t jobs, int64_t min_span_byt
 }
 
 struct CrcPlan {
-    int64_t groups, stripes;
+    int groups;
+    int64_t stripes;
     uint64_t pad;
 };
 
+// Stripes of `groups` 16 KiB groups: a record of at most 16 groups is one
+// stripe; longer ones take the stripe length in [16, 48] groups that
+// minimises the groups read (front padding included) plus about ten groups'
+// worth of per-lane multiply per stripe.
 CrcPlan crc_plan(uint64_t record_bytes) {
+    const uint64_t total = record_bytes ? (record_bytes + kCrcGroup - 1) / kCrcGroup : 1;
     CrcPlan plan;
-    plan.groups = record_bytes >= static_cast<uint64_t>(kStripeGroups) * kGroup ? kStripeGroups : 1;
-    const uint64_t stripe_bytes = static_cast<uint64_t>(plan.groups) * kGroup;
-    plan.stripes = static_cast<int64_t>((record_bytes + stripe_bytes - 1) / stripe_bytes);
-    if (plan.stripes == 0) plan.stripes = 1;
+    plan.groups = static_cast<int>(total);
+    if (total > static_cast<uint64_t>(kCrcMinGroups)) {
+        uint64_t best = ~uint64_t(0);
+        for (int g = kCrcMinGroups; g <= kCrcMaxGroups; ++g) {
+            const uint64_t cost = (total + g - 1) / g * (g + 10);
+            if (cost <= best) {
+                best = cost;
+                plan.groups = g;
+            }
+        }
+    }
+    const uint64_t stripe_bytes = static_cast<uint64_t>(plan.groups) * kCrcGroup;
+    plan.stripes = static_cast<int64_t>((total * kCrcGroup + stripe_bytes - 1) / stripe_bytes);
     plan.pad = static_cast<uint64_t>(plan.stripes) * stripe_bytes - record_bytes;
     return plan;
 }
@@ -986,11 +1082,13 @@ int kvsnap_crc32c_records(const void* records, uint64_t record_bytes, uint64_t r
         auto* partial = static_cast<uint32_t*>(workspace);
         const auto* base = static_cast<const uint8_t*>(records);
         if (aligned)
-            hipLaunchKernelGGL(crc_stripes_kernel<true>, dim3(grid), dim3(kThreads), 0, s, base, record_pitch, n_records, plan.stripes, plan.groups, plan.pad, partial);
+            hipLaunchKernelGGL(crc_stripes_kernel<true>, dim3(grid), dim3(kCrcThreads), 0, s, base, record_pitch,
+                               n_records, plan.stripes, plan.groups, plan.pad, partial);
         else
-            hipLaunchKernelGGL(crc_stripes_kernel<false>, dim3(grid), dim3(kThreads), 0, s, base, record_pitch, n_records, plan.stripes, plan.groups, plan.pad, partial);
+            hipLaunchKernelGGL(crc_stripes_kernel<false>, dim3(grid), dim3(kCrcThreads), 0, s, base, record_pitch,
+                               n_records, plan.stripes, plan.groups, plan.pad, partial);
         check_launch("crc32c stripes");
-        const uint32_t stripe_shift = host_xpow8n(static_cast<uint64_t>(plan.groups) * kGroup);
+        const uint32_t stripe_shift = host_xpow8n(static_cast<uint64_t>(plan.groups) * kCrcGroup);
         const uint32_t init_term = host_shift(~prior, record_bytes);
         hipLaunchKernelGGL(crc_combine_kernel, dim3(static_cast<unsigned>((n_records + 63) / 64)), dim3(64), 0, s,
                            partial, n_records, plan.stripes, stripe_shift, init_term, out);
