@@ -343,8 +343,8 @@ __global__ __launch_bounds__(kThreads) void synth_decode_kernel(const int64_t* _
 // combined by Horner's rule; crc32c = ~(shift(~prior, N) ^ R(record)).
 //
 // Inside a stripe, lane t of a 1024-lane workgroup reads the 16-byte word at
-// t*16 of every 16 KiB group (fully coalesced; a batch of 16 groups is loaded
-// before any is folded, so a lane has 16 loads in flight), folds them with
+// t*16 of every 16 KiB group (fully coalesced; a batch of 8 groups is loaded
+// before any is folded, so a lane has 8 loads in flight), folds them with
 //   acc = shift(acc, 16384) ^ R16(word),
 // and finally contributes shift(acc, (1023 - t) * 16); the workgroup's XOR of
 // those is the stripe's raw CRC.  R16 runs slicing-by-4 over the word's four
@@ -366,15 +366,18 @@ __global__ __launch_bounds__(kThreads) void synth_decode_kernel(const int64_t* _
 // 128 KiB of the 160 KiB LDS, so a CU holds one workgroup; the 4 KiB of G
 // stay shared (4 of the 20 lookups per word) at the front of the LDS, where
 // each table's base also fits the offset field.
-// A stripe is 16-48 groups (256-768 KiB), chosen per record size to keep the
-// zero padding in front of the first stripe small (Qwen3-8B records: three
-// 768 KiB stripes, no padding) and the per-lane multiply rare.
+// A stripe is 8-48 groups (128-768 KiB), chosen per record size and count
+// (crc_plan); groups that hold only front padding are skipped.  One batch in
+// flight per lane measured as fast as two (software-pipelined), and 8-group
+// batches beat 16 (5.6-5.9 against 5.2-5.6 TB/s): a 1024-lane workgroup with
+// 256 KiB of loads in flight is past what the memory system serves best, as
+// a plain read kernel of the same shape also shows.
 
 constexpr uint32_t kPoly = 0x82F63B78u;
 constexpr int kCrcThreads = 1024;
 constexpr int kCrcGroup = kCrcThreads * 16;  // bytes per group: one 16-byte word per lane
-constexpr int kCrcBatch = 16;                // groups loaded before they are folded
-constexpr int kCrcMinGroups = 16, kCrcMaxGroups = 48;
+constexpr int kCrcBatch = 8;                // groups loaded before they are folded
+constexpr int kCrcMaxGroups = (768 << 10) / kCrcGroup;  // stripes of at most 768 KiB
 constexpr int kCrcGrid = 256;                // persistent, one workgroup per CU
 constexpr int kCrcAdvanceBytes = 4 * 1024;   // G, shared, at LDS byte 0
 constexpr int kCrcPrivateBytes = 2 * 65536;  // the lanes' copies of S, after G
@@ -466,13 +469,14 @@ __global__ __launch_bounds__(kCrcThreads) void crc_stripes_kernel(const uint8_t*
             const int n = groups - g0 < kCrcBatch ? groups - g0 : kCrcBatch;  // workgroup-uniform
             const int64_t batch_at = j * stripe_bytes + static_cast<int64_t>(g0) * kCrcGroup - static_cast<int64_t>(pad);
             if (kAligned && n == kCrcBatch && batch_at >= 0) {
-                // Sixteen whole groups of the record: no padding, no predicates.  The words' slicing chains
+                // A whole batch of record groups: no padding, no predicates.  The words' slicing chains
                 // are independent, so they interleave; the advance chain follows.
                 const u32x4* at = reinterpret_cast<const u32x4*>(rec + batch_at) + threadIdx.x;
                 u32x4 v[kCrcBatch];
 #pragma unroll
                 for (int g = 0; g < kCrcBatch; ++g) v[g] = __builtin_nontemporal_load(at + g * (kCrcGroup / 16));
-                // Keep all sixteen loads ahead of the first fold (the scheduler would otherwise wait on the first).
+                // Keep all the batch's loads ahead of its first fold (the scheduler would otherwise wait on
+                // the first load before issuing the rest).
                 __builtin_amdgcn_sched_barrier(0);
                 uint32_t r[kCrcBatch];
 #pragma unroll
@@ -501,9 +505,11 @@ __global__ __launch_bounds__(kCrcThreads) void crc_stripes_kernel(const uint8_t*
                     v[g] = u32x4{w[0], w[1], w[2], w[3]};
                 }
             }
+            // Groups of padding only come first, while acc is still zero: they are skipped, not folded.
+            const int64_t lead = j == 0 ? static_cast<int64_t>(pad / kCrcGroup) : 0;
 #pragma unroll
             for (int g = 0; g < kCrcBatch; ++g)
-                if (g < n) acc = crc_advance(lds, acc) ^ crc_word(lds, cols, v[g]);
+                if (g < n && g0 + g >= lead) acc = crc_advance(lds, acc) ^ crc_word(lds, cols, v[g]);
         }
         uint32_t x = gf_mul(lane_shift, acc);
 #pragma unroll
@@ -916,18 +922,25 @@ struct CrcPlan {
     uint64_t pad;
 };
 
-// Stripes of `groups` 16 KiB groups: a record of at most 16 groups is one
-// stripe; longer ones take the stripe length in [16, 48] groups that
-// minimises the groups read (front padding included) plus about ten groups'
-// worth of per-lane multiply per stripe.
-CrcPlan crc_plan(uint64_t record_bytes) {
+// Stripes of `groups` 16 KiB groups, the first one padded in front.  A stripe
+// is one workgroup's job and costs its real groups plus about four groups'
+// worth of per-lane multiply and reduction; whole groups of padding cost
+// nothing.  The kCrcGrid resident workgroups take about ceil(jobs / kCrcGrid)
+// rounds, so the plan picks the multiple of kCrcBatch up to kCrcMaxGroups
+// that minimises rounds * (groups + 4): three 768 KiB stripes per Qwen3-8B
+// record for a 512-record session, smaller stripes when few records have to
+// fill the chip.
+CrcPlan crc_plan(uint64_t record_bytes, int64_t n_records) {
     const uint64_t total = record_bytes ? (record_bytes + kCrcGroup - 1) / kCrcGroup : 1;
+    const uint64_t n = n_records > 0 ? static_cast<uint64_t>(n_records) : 1;
     CrcPlan plan;
     plan.groups = static_cast<int>(total);
-    if (total > static_cast<uint64_t>(kCrcMinGroups)) {
+    if (total > static_cast<uint64_t>(kCrcBatch)) {
         uint64_t best = ~uint64_t(0);
-        for (int g = kCrcMinGroups; g <= kCrcMaxGroups; ++g) {
-            const uint64_t cost = (total + g - 1) / g * (g + 10);
+        for (int g = kCrcBatch; g <= kCrcMaxGroups; g += kCrcBatch) {
+            const uint64_t stripes = (total + g - 1) / g;
+            const uint64_t rounds = (n * stripes + kCrcGrid - 1) / kCrcGrid;
+            const uint64_t cost = rounds * (g + 4);
             if (cost <= best) {
                 best = cost;
                 plan.groups = g;
@@ -1062,7 +1075,8 @@ int kvsnap_synth_fill(uint64_t seed, int kind, const int64_t* span_bases, const 
 
 size_t kvsnap_crc32c_workspace_bytes(uint64_t record_bytes, int64_t n_records) {
     if (n_records <= 0) return 0;
-    return static_cast<size_t>(crc_plan(record_bytes).stripes) * static_cast<size_t>(n_records) * sizeof(uint32_t);
+    return static_cast<size_t>(crc_plan(record_bytes, n_records).stripes) * static_cast<size_t>(n_records) *
+           sizeof(uint32_t);
 }
 
 int kvsnap_crc32c_records(const void* records, uint64_t record_bytes, uint64_t record_pitch, int64_t n_records,
@@ -1071,7 +1085,7 @@ int kvsnap_crc32c_records(const void* records, uint64_t record_bytes, uint64_t r
         if (n_records < 0) throw std::runtime_error("negative record count");
         if (n_records == 0) return;
         if (!out || (!records && record_bytes)) throw std::runtime_error("CRC32C needs device pointers");
-        const CrcPlan plan = crc_plan(record_bytes);
+        const CrcPlan plan = crc_plan(record_bytes, n_records);
         const size_t need = static_cast<size_t>(plan.stripes) * static_cast<size_t>(n_records) * sizeof(uint32_t);
         if (!workspace || workspace_bytes < need) throw std::runtime_error("CRC32C workspace too small");
         ensure_crc_tables();
