@@ -378,7 +378,12 @@ constexpr int kCrcThreads = 1024;
 constexpr int kCrcGroup = kCrcThreads * 16;  // bytes per group: one 16-byte word per lane
 constexpr int kCrcBatch = 8;                // groups loaded before they are folded
 constexpr int kCrcMaxGroups = (768 << 10) / kCrcGroup;  // stripes of at most 768 KiB
-constexpr int kCrcGrid = 256;                // persistent, one workgroup per CU
+constexpr int kCrcResident = 256;            // workgroups resident at once: one per CU
+// Launch grid cap: twice the resident count.  Beside a save's SHA-256 kernels
+// (whose workgroups hold a CU's LDS) a one-per-CU persistent grid waits for
+// its last workgroups to find a CU (0.283 ms in the pipelined step against
+// 0.250 at 512 and 0.241 with one workgroup per job, which costs 8 % alone).
+constexpr int kCrcGrid = 512;
 constexpr int kCrcAdvanceBytes = 4 * 1024;   // G, shared, at LDS byte 0
 constexpr int kCrcPrivateBytes = 2 * 65536;  // the lanes' copies of S, after G
 
@@ -925,8 +930,8 @@ struct CrcPlan {
 // Stripes of `groups` 16 KiB groups, the first one padded in front.  A stripe
 // is one workgroup's job and costs its real groups plus about four groups'
 // worth of per-lane multiply and reduction; whole groups of padding cost
-// nothing.  The kCrcGrid resident workgroups take about ceil(jobs / kCrcGrid)
-// rounds, so the plan picks the multiple of kCrcBatch up to kCrcMaxGroups
+// nothing.  The kCrcResident resident workgroups take about
+// ceil(jobs / kCrcResident) rounds, so the plan picks the multiple of kCrcBatch up to kCrcMaxGroups
 // that minimises rounds * (groups + 4): three 768 KiB stripes per Qwen3-8B
 // record for a 512-record session, smaller stripes when few records have to
 // fill the chip.
@@ -939,7 +944,7 @@ CrcPlan crc_plan(uint64_t record_bytes, int64_t n_records) {
         uint64_t best = ~uint64_t(0);
         for (int g = kCrcBatch; g <= kCrcMaxGroups; g += kCrcBatch) {
             const uint64_t stripes = (total + g - 1) / g;
-            const uint64_t rounds = (n * stripes + kCrcGrid - 1) / kCrcGrid;
+            const uint64_t rounds = (n * stripes + kCrcResident - 1) / kCrcResident;
             const uint64_t cost = rounds * (g + 4);
             if (cost <= best) {
                 best = cost;

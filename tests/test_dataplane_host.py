@@ -398,9 +398,10 @@ def test_digests_are_returned_in_block_order():
     plane = register(caches)
     size = plane.block_bytes
 
-    def emulated_digests(torch_module, records_ptr, record_bytes, record_pitch, n, device, stream, timer=None):
+    def emulated_digests(torch_module, records_ptr, record_bytes, record_pitch, n, device, stream, timer=None,
+                         crc_stream=None):
         crcs, shas = oracle.digest_records(records_ptr, record_bytes, record_pitch, n)
-        return (torch.from_numpy(crcs.astype(np.int64)), torch.from_numpy(shas), None)
+        return (torch.from_numpy(crcs.astype(np.int64)), torch.from_numpy(shas), torch.empty(16, dtype=torch.uint8))
 
     targets = targets_for("staging", 3, size)
     digests = []
