@@ -73,6 +73,14 @@ int kvsnap_scatter_blocks(const void* records, int64_t record_pitch, const int64
                           const int64_t* span_words, int64_t n_spans, int64_t min_span_bytes, int programs,
                           uintptr_t stream);
 
+/* Copy nbytes from pinned host memory to device memory on `stream` (the DMA
+ * engines, hipMemcpyAsync).  The restore's "dma" mode stages records with it
+ * and then scatters them with kvsnap_scatter_blocks, so that a restore's
+ * host-to-device traffic runs on the copy engines beside a save's
+ * device-to-host copies; the reference has no counterpart (its restore reads
+ * pinned memory in place, kvsnap/connector/copy_kernel.py:22-40). */
+int kvsnap_copy_to_device(void* dst, const void* src, size_t nbytes, uintptr_t stream);
+
 /* Zero n byte ranges [base + offsets[i], + lengths[i]): the token slots past
  * the last computed token of a record.  Replaces the host memsets of
  * TorchBlockDataPlane._zero_tail, kvsnap/connector/dataplane.py:262-272. */

@@ -496,3 +496,19 @@ def test_restore_progress_reaches_the_early_report_threshold_at_the_expected_lau
                                        for k in range(-(-512 // per_launch))]
     assert len(progress) - 1 == 19
     assert early_launch_index(progress) == 16
+
+
+def test_restore_runs_group_consecutive_records():
+    """The DMA restore copies each run of adjacent pinned records with one copy."""
+    from kvsnap_amd.dataplane import _runs
+    assert _runs([0, 10, 20, 40, 50, 70], 10) == [(0, 3), (3, 2), (5, 1)]
+    assert _runs([100, 110, 200], 10, 5) == [(5, 2), (7, 1)]
+    assert _runs([30, 20, 10], 10) == [(0, 1), (1, 1), (2, 1)]
+    assert _runs([], 10) == []
+
+
+def test_restore_mode_is_checked():
+    caches = {"layer.0": CudaLabelled(torch.zeros(4, 2, BLOCK_SIZE, 8))}
+    with patch.dict(sys.modules, {"torch": CpuTorch()}), patch.object(dataplane, "CudaPool", return_value=HostPool()):
+        with pytest.raises(ValueError, match="restore_mode"):
+            TorchBlockDataPlane(caches, BLOCK_SIZE, 1 << 30, restore_mode="fast")

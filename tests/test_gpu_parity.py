@@ -59,10 +59,12 @@ def pinned_bytes(allocation, offset, size):
     return np.frombuffer(C.string_at(allocation.pointer + offset, size), dtype=np.uint8)
 
 
-def test_a_saved_snapshot_restores_bit_for_bit_into_shuffled_blocks(planes):
-    """The reference's own GPU case (test_copy_kernel_cuda.py:41-63), on the HIP kernels."""
+@pytest.mark.parametrize("restore_mode", ["kernel", "dma"])
+def test_a_saved_snapshot_restores_bit_for_bit_into_shuffled_blocks(planes, restore_mode):
+    """The reference's own GPU case (test_copy_kernel_cuda.py:41-63), on the HIP kernels: the restore kernel
+    reading pinned records in place, or the copy engines staging them for the scatter kernel."""
     backing, caches = vllm_caches(LAYERS, BLOCKS)
-    plane = planes(caches)
+    plane = planes(caches, restore_mode=restore_mode)
     rng = random.Random(1)
     saved = rng.sample(range(1, BLOCKS), 20)
     restored = rng.sample([b for b in range(1, BLOCKS) if b not in saved], 20)
@@ -85,6 +87,71 @@ def test_a_saved_snapshot_restores_bit_for_bit_into_shuffled_blocks(planes):
         backing.view(torch.int16).copy_(before)
         for allocation in owned:
             allocation.close()
+
+
+def test_saves_and_restores_from_two_threads_overlap_byte_exact(planes):
+    """The connector's save thread and loader thread at once (reference vllm.py:202-203), restores on their
+    own stream through the copy engines: session k is restored while session k + 1 is saved into the other
+    pinned buffer.  Every restore must hold exactly the bytes its save saw."""
+    import threading
+    caches, backing = synth.make_caches(LAYERS, 96, layout="kv_split")
+    plane = planes(caches, capacity=2 * 16 * LAYERS * 65536 + (64 << 20), restore_stream="split",
+                   restore_mode="dma")
+    rng = random.Random(8)
+    source = rng.sample(range(1, 96), 16)
+    target = rng.sample([b for b in range(1, 96) if b not in source], 16)
+    assert max(source + target) < backing.shape[2]       # [layers, 2, blocks, N, H, D]
+    size = plane.block_bytes
+    buffers = [plane.pool.reserve(16 * size) for _ in range(2)]
+    targets = [[(b, i * size) for i in range(16)] for b in buffers]
+    steps = 6
+    saved = [threading.Event() for _ in range(steps)]
+    restored = [threading.Event() for _ in range(steps)]
+    expected, failures, digests = {}, [], []
+    src = torch.tensor(source, device="cuda")
+    dst = torch.tensor(target, device="cuda")
+
+    def saver():
+        try:
+            for k in range(steps):
+                if k >= 2:
+                    restored[k - 2].wait(60)
+                keep = [synth.fill(plane, 100 + k, first_block=b, num_blocks=1) for b in source]
+                expected[k] = backing[:, :, src].clone()
+                plane.save_gather(source, targets[k % 2], 16 * BLOCK_SIZE, digests=digests)
+                del keep
+                saved[k].set()
+        except BaseException as exc:
+            failures.append(exc)
+            for event in saved:
+                event.set()
+
+    def loader():
+        try:
+            for k in range(steps):
+                saved[k].wait(60)
+                if failures:
+                    return
+                plane.load_scatter(target, targets[k % 2], chunk_bytes=5 * size)
+                torch.cuda.synchronize()
+                if not torch.equal(backing[:, :, dst].view(torch.int16), expected[k].view(torch.int16)):
+                    failures.append(AssertionError(f"restore {k} differs from save {k}"))
+                restored[k].set()
+        except BaseException as exc:
+            failures.append(exc)
+            for event in restored:
+                event.set()
+
+    threads = [threading.Thread(target=saver), threading.Thread(target=loader)]
+    for t in threads:
+        t.start()
+    for t in threads:
+        t.join(120)
+    assert not any(t.is_alive() for t in threads)
+    assert not failures, failures
+    assert len({tuple(d.result()) for d in digests[-1:]}) == 1
+    for b in buffers:
+        b.close()
 
 
 @pytest.mark.parametrize("layout", ["vllm", "kv_split"])
