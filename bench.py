@@ -467,10 +467,14 @@ def run_rotating(args):
                                         dtype=torch.float8_e4m3fn)
     sessions_tokens = [1024, 2048, 4096, 8192]
     size = layers * 32768
-    # Copies beside decode: direct saves on 8-workgroup grids moved 27 GB/s with the decode median within 4 %;
-    # staged saves on 64-workgroup grids moved 14 GB/s there, and are faster only when nothing else runs.
+    # Copies beside decode: direct saves on 4-workgroup grids and restores through the copy engines moved
+    # 41 GB/s with a 0.17 ms p99 decode stall.  The restore kernel reading pinned memory in place holds CUs
+    # through the link's latency and stalled the decode 0.85 ms at p99; staged saves (full-grid gathers)
+    # moved only 14 GB/s beside it.
     plane = TorchBlockDataPlane(caches, block_size, sum(t // block_size for t in sessions_tokens) * size + (64 << 20),
-                                save_mode=args.save_mode or "direct", restore_programs=args.programs or 8)
+                                save_mode=args.save_mode or "direct", restore_programs=args.programs or 4,
+                                restore_mode=args.restore_mode or "dma",
+                                gather_programs=args.gather_programs)
     plane.warm_up()
     scales_rng = random.Random(4)
     layer_inv = [scales_rng.uniform(0.5, 2.0) for _ in range(layers)]
@@ -555,9 +559,12 @@ def run_rotating(args):
                                "loaded_p99": round(percentile(loaded, 99), 4), "steps": len(loaded)},
             "decode_hbm_gbps_baseline": round(step_bytes / base_med / 1e6, 1),
             "p99_compute_stall_ms": round(percentile(stalls, 99), 4),
-            "save_mode": plane.save_mode, "restore_programs": plane.restore_programs, "byte_exact": exact,
-            "note": "beside this decode, staged saves with 64-workgroup grids moved 14 GB/s (p99 stall 0.95 ms); "
-                    "direct saves with 8 moved 27 GB/s (0.51 ms), with 10 or more the decode median rose 29-70 %"}
+            "save_mode": plane.save_mode, "restore_programs": plane.restore_programs,
+            "restore_mode": plane.restore_mode, "gather_programs": plane.gather_programs, "byte_exact": exact,
+            "note": "beside this decode (median / p99 stall): direct saves on 4 workgroups with copy-engine "
+                    "restores 41 GB/s (+10 % / 0.17 ms), on 2-3 workgroups 30-36 GB/s (+9 % / 0.11 ms), on 6 "
+                    "39 GB/s (0.71 ms); with the in-place restore kernel on 4 workgroups 29 GB/s (+21 % / 0.85 ms); "
+                    "staged saves 14 GB/s"}
 
 
 # ---------------------------------------------------------------- save and restore overlapped on the link
@@ -962,11 +969,13 @@ def main():
     parser.add_argument("--save-mode", choices=("staged", "direct"), default=None,
                         help="rotating-fp8: save mode of the plane (default direct)")
     parser.add_argument("--programs", type=int, default=None,
-                        help="rotating-fp8: restore / direct-save workgroups (default 8)")
+                        help="rotating-fp8: restore / direct-save workgroups (default 4)")
+    parser.add_argument("--gather-programs", type=int, default=None,
+                        help="rotating-fp8: workgroups of the plane's gather and scatter grids (default 0: one per job)")
     parser.add_argument("--no-digests", action="store_true",
                         help="duplex: saves without GPU CRC32C / SHA-256 (the link alone)")
     parser.add_argument("--restore-mode", choices=("kernel", "dma"), default=None,
-                        help="duplex: how restores cross the link (default dma)")
+                        help="duplex, rotating-fp8: how restores cross the link")
     parser.add_argument("--disk-dir", default=None, help="disk-fork, turns: where the blob files go")
     parser.add_argument("--cpu-seconds", type=float, default=20.0)
     parser.add_argument("--no-cpu-baseline", action="store_true")
