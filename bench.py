@@ -527,12 +527,16 @@ def run_rotating(args):
     base_med, base_p99 = statistics.median(baseline), percentile(baseline, 99)
     moved = [0]
 
+    digests = []
+
     def rotate(rounds):
         for _ in range(rounds):
             for tokens, src, dst, staged, targets in sessions:
-                plane.save_gather(src, targets, tokens)
+                plane.save_gather(src, targets, tokens, digests=digests if args.digests else None)
                 plane.load_scatter(dst, targets)
                 moved[0] += 2 * len(src) * size
+        for d in digests:
+            d.result()
 
     t0 = time.perf_counter()
     rotate(1)                                           # copies alone
@@ -561,6 +565,7 @@ def run_rotating(args):
             "p99_compute_stall_ms": round(percentile(stalls, 99), 4),
             "save_mode": plane.save_mode, "restore_programs": plane.restore_programs,
             "restore_mode": plane.restore_mode, "gather_programs": plane.gather_programs, "byte_exact": exact,
+            "saves_hashed": bool(args.digests),
             "note": "beside this decode (median / p99 stall): direct saves on 4 workgroups with copy-engine "
                     "restores 41 GB/s (+10 % / 0.17 ms), on 2-3 workgroups 30-36 GB/s (+9 % / 0.11 ms), on 6 "
                     "39 GB/s (0.71 ms); with the in-place restore kernel on 4 workgroups 29 GB/s (+21 % / 0.85 ms); "
@@ -972,6 +977,8 @@ def main():
                         help="rotating-fp8: restore / direct-save workgroups (default 4)")
     parser.add_argument("--gather-programs", type=int, default=None,
                         help="rotating-fp8: workgroups of the plane's gather and scatter grids (default 0: one per job)")
+    parser.add_argument("--digests", action="store_true",
+                        help="rotating-fp8: every save also computes its CRC32C and SHA-256 on the GPU")
     parser.add_argument("--no-digests", action="store_true",
                         help="duplex: saves without GPU CRC32C / SHA-256 (the link alone)")
     parser.add_argument("--restore-mode", choices=("kernel", "dma"), default=None,
