@@ -497,6 +497,46 @@ def test_qwen3_8b_8k_session_at_full_size(planes, oracle_lib):
     staged.close()
 
 
+@pytest.mark.parametrize("layout", ["kv_split", "vllm"])
+@pytest.mark.parametrize("restore_mode", ["kernel", "dma"])
+def test_a_tensor_parallel_shard_round_trips_with_short_spans(planes, oracle_lib, layout, restore_mode):
+    """One TP = 8 rank's shard of Qwen3-8B (1 KV head: 4 KiB K/V spans, 8 KiB vLLM spans), where the copy
+    launches put several spans in one workgroup: the gathered records equal the oracle's fill, their
+    digests the oracle's, and the restore is the identity, through the restore kernel and the copy engines."""
+    caches, backing = synth.make_caches(36, 600, heads=1, layout=layout)
+    plane = planes(caches, capacity=128 * 36 * 8192 + (64 << 20), restore_mode=restore_mode)
+    assert plane.min_span_bytes == (4096 if layout == "kv_split" else 8192)
+    keep = synth.fill(plane, 3)
+    torch.cuda.synchronize()
+    del keep
+    size = plane.block_bytes
+    assert size == 36 * 8192
+    saved, restored = synth.block_tables(600, 128, seed_source=5, seed_target=6)
+    assert max(saved + restored) < 600
+    staged = plane.pool.reserve(128 * size)
+    targets = [(staged, i * size) for i in range(128)]
+    digests = []
+    plane.save_gather(saved, targets, 128 * 16 - 5, digests=digests)
+    got = digests[0].result()
+    crcs, shas = oracle_lib.digest_records(staged.pointer, size, size, 128, threads=16)
+    assert [crc for _, crc in got] == crcs.tolist()
+    assert [sha for sha, _ in got] == [bytes(h).hex() for h in shas]
+    for index in (0, 77):
+        record = pinned_bytes(staged, index * size, size)
+        for s, (offset, _, _, nbytes) in enumerate(plane.spans()):
+            assert np.array_equal(record[offset:offset + nbytes],
+                                  oracle_lib.fill_span(3, s, saved[index], nbytes, synth.KIND_BF16)), (index, s)
+    plane.load_scatter(restored, targets, chunk_bytes=40 * size)
+    torch.cuda.synchronize()
+    src, dst = torch.tensor(saved[:-1], device="cuda"), torch.tensor(restored[:-1], device="cuda")
+    for view in caches.values():
+        if layout == "kv_split":               # [2, blocks, N, H, D]
+            assert torch.equal(view[:, src].view(torch.int16), view[:, dst].view(torch.int16))
+        else:                                   # [blocks, H, N, 2D]
+            assert torch.equal(view[src].view(torch.int16), view[dst].view(torch.int16))
+    staged.close()
+
+
 def test_an_early_reported_restore_is_complete_for_the_engine_stream(planes):
     """The connector's protocol (reference vllm.py:454-466, 663-679): a loader thread runs the restore while the
     engine polls its progress; at most 128 MiB left, the load is reported and the next forward waits on the last
