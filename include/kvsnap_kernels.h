@@ -103,6 +103,20 @@ int kvsnap_crc32c_records(const void* records, uint64_t record_bytes, uint64_t r
 int kvsnap_sha256_records(const void* records, uint64_t record_bytes, uint64_t record_pitch, int64_t n_records,
                           uint8_t* out, uintptr_t stream);
 
+/* 64-byte compressions in one record's SHA-256 chain, padding included. */
+uint64_t kvsnap_sha256_blocks(uint64_t record_bytes);
+
+/* Compressions [first_block, end_block) of every record's SHA-256 chain:
+ * from the initial value when first_block = 0, else from `state` (8 uint32
+ * per record, left there by the previous range); the digest into `out` when
+ * end_block = kvsnap_sha256_blocks(record_bytes), else the chaining state
+ * back into `state`.  A series of ranges equals one kvsnap_sha256_records
+ * call; each launch is short, so the stream's hardware queue (which other
+ * streams of the process may share) is never held for a whole chain. */
+int kvsnap_sha256_records_range(const void* records, uint64_t record_bytes, uint64_t record_pitch,
+                                int64_t n_records, uint64_t first_block, uint64_t end_block, uint32_t* state,
+                                uint8_t* out, uintptr_t stream);
+
 /* Seeded synthetic KV for benchmarks and tests (no reference counterpart):
  * every span of blocks [first_block, first_block + n_blocks) filled from a
  * counter-based generator keyed (seed, span, block, element); kind 0 bf16

@@ -765,10 +765,18 @@ __device__ __forceinline__ void sha_produce(const uint8_t* __restrict__ p, uint6
     sha_schedule(w, slot, lane);
 }
 
+// Blocks [b0, b1) of every record's chain.  b0 = 0 starts from the FIPS
+// 180-4 initial value, otherwise from `state` (8 words per record, as a
+// previous launch left them); b1 = nblocks writes the digest to `out`,
+// otherwise the chaining state back to `state`.  A whole hash in one launch
+// holds its stream (and any stream sharing its hardware queue) for the whole
+// chain; the host can run it as a series of shorter launches instead.
 template <bool kAligned>
 __global__ __launch_bounds__(kShaThreads) void sha256_kernel(const uint8_t* __restrict__ records,
                                                              uint64_t record_bytes, uint64_t pitch,
-                                                             int64_t n_records, uint32_t* __restrict__ out) {
+                                                             int64_t n_records, uint64_t b0, uint64_t b1,
+                                                             uint32_t* __restrict__ state,
+                                                             uint32_t* __restrict__ out) {
     __shared__ u32x4 sched[2][kShaStep][kShaBlockQuads][kShaColumns];
     const bool producer = threadIdx.x >= 128;
     const int lane = threadIdx.x & 63;
@@ -783,7 +791,8 @@ __global__ __launch_bounds__(kShaThreads) void sha256_kernel(const uint8_t* __re
     const uint64_t whole = record_bytes / 64;
     const int nfinal = record_bytes - 64 * whole + 9 <= 64 ? 1 : 2;
     const uint64_t nblocks = whole + nfinal;
-    const uint64_t steps = (nblocks + kShaStep - 1) / kShaStep;
+    const uint64_t span = b1 - b0;
+    const uint64_t steps = (span + kShaStep - 1) / kShaStep;
     uint32_t raw[kShaStep][16];
     if (producer) {
         for (int i = lane; i < 2 * kShaStep * kShaBlockQuads; i += 64) {
@@ -792,40 +801,48 @@ __global__ __launch_bounds__(kShaThreads) void sha256_kernel(const uint8_t* __re
         }
 #pragma unroll
         for (int i = 0; i < kShaStep; ++i)
-            if (static_cast<uint64_t>(i) < nblocks) sha_message_raw<kAligned>(p, record_bytes, whole, nfinal, i, raw[i]);
+            if (static_cast<uint64_t>(i) < span) sha_message_raw<kAligned>(p, record_bytes, whole, nfinal, b0 + i, raw[i]);
 #pragma unroll
         for (int i = 0; i < kShaStep; ++i)
-            if (static_cast<uint64_t>(i) < nblocks)
-                sha_produce<kAligned>(p, record_bytes, whole, nfinal, nblocks, i, raw[i], sched[0][i], lane);
+            if (static_cast<uint64_t>(i) < span)
+                sha_produce<kAligned>(p, record_bytes, whole, nfinal, b1, b0 + i, raw[i], sched[0][i], lane);
     }
     __syncthreads();
     ShaHalf half = a_lane ? ShaHalf{2, 13, 22, ~0u} : ShaHalf{6, 11, 25, 0u};
     opaque(half.m);
     uint32_t x[4];
-    if (a_lane) {
+    uint32_t* chain = state ? state + 8 * (live ? r : 0) + (a_lane ? 0 : 4) : nullptr;
+    if (b0 > 0) {
+        const u32x4 h = *reinterpret_cast<const u32x4*>(chain);
+        x[0] = h.x; x[1] = h.y; x[2] = h.z; x[3] = h.w;
+    } else if (a_lane) {
         x[0] = 0x6a09e667; x[1] = 0xbb67ae85; x[2] = 0x3c6ef372; x[3] = 0xa54ff53a;
     } else {
         x[0] = 0x510e527f; x[1] = 0x9b05688c; x[2] = 0x1f83d9ab; x[3] = 0x5be0cd19;
     }
     const int column = a_lane ? 64 : rec;
     for (uint64_t step = 0; step < steps; ++step) {
-        const uint64_t first = step * kShaStep;
+        const uint64_t first = b0 + step * kShaStep;
         if (producer) {
 #pragma unroll
             for (int i = 0; i < kShaStep; ++i)
-                if (first + kShaStep + i < nblocks)
-                    sha_produce<kAligned>(p, record_bytes, whole, nfinal, nblocks, first + kShaStep + i, raw[i],
+                if (first + kShaStep + i < b1)
+                    sha_produce<kAligned>(p, record_bytes, whole, nfinal, b1, first + kShaStep + i, raw[i],
                                           sched[(step + 1) & 1][i], lane);
         } else {
 #pragma unroll
             for (int i = 0; i < kShaStep; ++i)
-                if (first + i < nblocks) sha_rounds_pair(x, sched[step & 1][i], column, half);
+                if (first + i < b1) sha_rounds_pair(x, sched[step & 1][i], column, half);
         }
         __syncthreads();
     }
-    if (!producer && live)
-        *reinterpret_cast<u32x4*>(out + 8 * r + (a_lane ? 0 : 4)) =
-            u32x4{bswap(x[0]), bswap(x[1]), bswap(x[2]), bswap(x[3])};
+    if (!producer && live) {
+        if (b1 == nblocks)
+            *reinterpret_cast<u32x4*>(out + 8 * r + (a_lane ? 0 : 4)) =
+                u32x4{bswap(x[0]), bswap(x[1]), bswap(x[2]), bswap(x[3])};
+        else
+            *reinterpret_cast<u32x4*>(chain) = u32x4{x[0], x[1], x[2], x[3]};
+    }
 }
 
 // ----------------------------------------------------------------- host helpers
@@ -1125,26 +1142,44 @@ int kvsnap_crc32c_records(const void* records, uint64_t record_bytes, uint64_t r
     });
 }
 
-int kvsnap_sha256_records(const void* records, uint64_t record_bytes, uint64_t record_pitch, int64_t n_records,
-                          uint8_t* out, uintptr_t stream) {
+uint64_t kvsnap_sha256_blocks(uint64_t record_bytes) {
+    const uint64_t whole = record_bytes / 64;
+    return whole + (record_bytes - 64 * whole + 9 <= 64 ? 1 : 2);
+}
+
+int kvsnap_sha256_records_range(const void* records, uint64_t record_bytes, uint64_t record_pitch,
+                                int64_t n_records, uint64_t first_block, uint64_t end_block, uint32_t* state,
+                                uint8_t* out, uintptr_t stream) {
     return guard([&] {
         if (n_records < 0) throw std::runtime_error("negative record count");
         if (n_records == 0) return;
-        if (!out || (!records && record_bytes)) throw std::runtime_error("SHA-256 needs device pointers");
-        if (reinterpret_cast<uintptr_t>(out) % 16) throw std::runtime_error("SHA-256 output must be 16-byte aligned");
+        const uint64_t nblocks = kvsnap_sha256_blocks(record_bytes);
+        if (first_block >= end_block || end_block > nblocks) throw std::runtime_error("SHA-256 block range out of order");
+        if (!records && record_bytes) throw std::runtime_error("SHA-256 needs device pointers");
+        if (end_block == nblocks && !out) throw std::runtime_error("SHA-256 needs an output for the last blocks");
+        if ((first_block > 0 || end_block < nblocks) && !state)
+            throw std::runtime_error("SHA-256 over part of the chain needs a state buffer");
+        if (reinterpret_cast<uintptr_t>(out) % 16 || reinterpret_cast<uintptr_t>(state) % 16)
+            throw std::runtime_error("SHA-256 output and state must be 16-byte aligned");
         hipStream_t s = reinterpret_cast<hipStream_t>(stream);
         const bool aligned = (reinterpret_cast<uintptr_t>(records) % 16 == 0) && (record_pitch % 16 == 0);
         const unsigned grid = static_cast<unsigned>((n_records + 63) / 64);
         const auto* base = static_cast<const uint8_t*>(records);
         auto* words = reinterpret_cast<uint32_t*>(out);
         if (aligned)
-            hipLaunchKernelGGL(sha256_kernel<true>, dim3(grid), dim3(kShaThreads), 0, s, base, record_bytes, record_pitch,
-                               n_records, words);
+            hipLaunchKernelGGL(sha256_kernel<true>, dim3(grid), dim3(kShaThreads), 0, s, base, record_bytes,
+                               record_pitch, n_records, first_block, end_block, state, words);
         else
-            hipLaunchKernelGGL(sha256_kernel<false>, dim3(grid), dim3(kShaThreads), 0, s, base, record_bytes, record_pitch,
-                               n_records, words);
+            hipLaunchKernelGGL(sha256_kernel<false>, dim3(grid), dim3(kShaThreads), 0, s, base, record_bytes,
+                               record_pitch, n_records, first_block, end_block, state, words);
         check_launch("sha256");
     });
+}
+
+int kvsnap_sha256_records(const void* records, uint64_t record_bytes, uint64_t record_pitch, int64_t n_records,
+                          uint8_t* out, uintptr_t stream) {
+    return kvsnap_sha256_records_range(records, record_bytes, record_pitch, n_records, 0,
+                                       kvsnap_sha256_blocks(record_bytes), nullptr, out, stream);
 }
 
 }  // extern "C"

@@ -398,14 +398,23 @@ def test_digests_are_returned_in_block_order():
     plane = register(caches)
     size = plane.block_bytes
 
-    def emulated_digests(torch_module, records_ptr, record_bytes, record_pitch, n, device, stream, timer=None,
-                         crc_stream=None):
-        crcs, shas = oracle.digest_records(records_ptr, record_bytes, record_pitch, n)
-        return (torch.from_numpy(crcs.astype(np.int64)), torch.from_numpy(shas), torch.empty(16, dtype=torch.uint8))
+    class EmulatedHashJob:
+        """The oracle in place of the GPU hash job, with its interface."""
+
+        def __init__(self, torch_module, records_ptr, record_bytes, record_pitch, n, device, stream, slice_blocks, *,
+                     timer=None, keepalive=None):
+            crcs, shas = oracle.digest_records(records_ptr, record_bytes, record_pitch, n)
+            self.crc, self.sha = torch.from_numpy(crcs.astype(np.int64)), torch.from_numpy(shas)
+
+        def query(self):
+            return True
+
+        def synchronize(self):
+            pass
 
     targets = targets_for("staging", 3, size)
     digests = []
-    with patch.object(dataplane, "digest_device_records", emulated_digests), \
+    with patch.object(dataplane, "HashJob", EmulatedHashJob), \
          patch.object(torch.Tensor, "record_stream", lambda self, stream: None):
         plane.save_gather([5, 2, 4], targets, 3 * BLOCK_SIZE - 2, digests=digests)
     result = digests[0].result()

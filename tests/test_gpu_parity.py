@@ -253,6 +253,40 @@ def test_sha256_kernel_covers_every_lane_of_both_round_waves(hip_library, oracle
     del workspace
 
 
+@pytest.mark.parametrize("record_bytes", [0, 55, 56, 119, 120, 1000, 4097, 65552])
+@pytest.mark.parametrize("shift", [0, 3])
+def test_sha256_over_block_ranges_equals_one_pass(hip_library, oracle_lib, record_bytes, shift):
+    """A chain run as several launches (state carried between them) gives the one-launch digest and hashlib's:
+    ranges of 1, 3, 4 and 7 compressions, ranges that hold only the padding blocks, aligned and unaligned."""
+    lib = kernel_library()
+    n, pitch = 70, record_bytes + 16
+    nblocks = int(lib.kvsnap_sha256_blocks(record_bytes))
+    assert nblocks == record_bytes // 64 + (1 if record_bytes % 64 + 9 <= 64 else 2)
+    data = torch.randint(0, 256, (n * pitch + 16,), dtype=torch.uint8, device="cuda")
+    base = data.data_ptr() + shift
+    stream = torch.cuda.current_stream().cuda_stream
+    whole = torch.zeros((n, 32), dtype=torch.uint8, device="cuda")
+    _check(lib, lib.kvsnap_sha256_records(base, record_bytes, pitch, n, whole.data_ptr(), stream))
+    host = data.cpu().numpy()
+    expected = [hashlib.sha256(host[shift + r * pitch: shift + r * pitch + record_bytes].tobytes()).digest()
+                for r in range(n)]
+    for step in (1, 3, 4, 7):
+        state = torch.zeros((n, 8), dtype=torch.int32, device="cuda")
+        out = torch.zeros((n, 32), dtype=torch.uint8, device="cuda")
+        bounds = list(range(0, nblocks, step)) + [nblocks]
+        for first, end in zip(bounds, bounds[1:]):
+            _check(lib, lib.kvsnap_sha256_records_range(base, record_bytes, pitch, n, first, end, state.data_ptr(),
+                                                        out.data_ptr(), stream))
+        torch.cuda.synchronize()
+        assert torch.equal(out, whole), (record_bytes, shift, step)
+        assert [bytes(out[r].cpu().numpy()) for r in range(n)] == expected, (record_bytes, shift, step)
+    # Ranges out of order, past the chain, or missing their state are refused.
+    for first, end, state_ptr in ((1, 1, 1), (0, nblocks + 1, 1), (1, nblocks, 0)):
+        with pytest.raises(RuntimeError):
+            _check(lib, lib.kvsnap_sha256_records_range(base, record_bytes, pitch, n, first, end,
+                                                        state_ptr and whole.data_ptr(), whole.data_ptr(), stream))
+
+
 def test_crc32c_kernel_extends_a_prior_value(hip_library, oracle_lib):
     lib = kernel_library()
     data = torch.randint(0, 256, (3 * 70000,), dtype=torch.uint8, device="cuda")
