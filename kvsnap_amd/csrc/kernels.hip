@@ -111,7 +111,12 @@ __device__ __forceinline__ JobLanes job_lanes(int lane_shift) {
 // CUs to the engine.
 constexpr int kRestoreThreads = 256, kRestoreUnroll = 8;
 // Gather: HBM to HBM, 1024-lane workgroups with 4 loads in flight per lane
-// (64 KiB per pass), the fastest shape measured.
+// (64 KiB per pass), the fastest shape measured.  A 32 KiB span takes the
+// whole workgroup, 2 loads per lane.  Tried and slower on the 8k Qwen3-8B
+// gather: an unroll of 8 (512 lanes per span, 4 loads each; 106 SGPRs, one
+// workgroup per CU: 5.1 against 5.9 TB/s), and global-address-space loads
+// and stores in place of the flat ones the table addresses compile to (equal
+// on 32 KiB spans, 5.6 against 5.9 TB/s on 64 KiB ones).
 constexpr int kGatherThreads = 1024, kGatherUnroll = 4;
 // Scatter from device records: HBM to HBM like the gather, writes scattered.
 constexpr int kScatterThreads = 1024, kScatterUnroll = 4;
