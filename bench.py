@@ -599,7 +599,8 @@ def run_duplex(args):
     session = tokens // block_size
     caches, backing = synth.make_caches(layers, num_blocks, block_size=block_size, layout=args.layout)
     plane = TorchBlockDataPlane(caches, block_size, 2 * session * layers * 65536 + (64 << 20),
-                                restore_stream="split", restore_mode=args.restore_mode or "dma")
+                                restore_stream="split", restore_mode=args.restore_mode or "dma",
+                                save_mode=args.save_mode)
     plane.warm_up()
     keep = synth.fill(plane, 0)
     torch.cuda.synchronize()
@@ -690,6 +691,7 @@ def run_duplex(args):
             "value": round(2 * total / (ms_per_step * 1e6), 3), "unit": "GB/s", "steps": args.steps,
             "warmup": args.warmup, "ms_per_step": round(ms_per_step, 3), "snapshot_bytes": total,
             "duplex_link_gbps": round(max(duplex), 2), "layout": args.layout, "restore_mode": plane.restore_mode,
+            "save_mode": plane.save_mode,
             "parity": {"restore_byte_exact": exact, "digests_bit_exact": digests_exact},
             "note": "session k restored while session k + 1 is saved (two host threads, two pinned buffers); "
                     "each step still saves 1.208 GB with CRC32C + SHA-256 and restores 1.208 GB"}
@@ -983,7 +985,7 @@ def main():
     parser.add_argument("--rounds", type=int, default=4, help="rotating-fp8: rounds over the four sessions")
     parser.add_argument("--turns", type=int, default=6, help="turns: turns after the first save")
     parser.add_argument("--save-mode", choices=("staged", "direct"), default=None,
-                        help="rotating-fp8: save mode of the plane (default direct)")
+                        help="rotating-fp8, duplex: save mode of the plane (rotating-fp8 default direct, duplex staged)")
     parser.add_argument("--programs", type=int, default=None,
                         help="rotating-fp8: restore / direct-save workgroups (default 4)")
     parser.add_argument("--gather-programs", type=int, default=None,

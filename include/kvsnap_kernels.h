@@ -117,6 +117,17 @@ int kvsnap_sha256_records_range(const void* records, uint64_t record_bytes, uint
                                 int64_t n_records, uint64_t first_block, uint64_t end_block, uint32_t* state,
                                 uint8_t* out, uintptr_t stream);
 
+/* Streams of the data plane's own (no reference counterpart; the reference
+ * copies on one stream).  kvsnap_stream_create makes a non-blocking stream of
+ * default priority on `device`; kvsnap_stream_destroy waits for its work and
+ * frees it.  kvsnap_hold_stream queues one wave that sleeps `iters` rounds of
+ * about 3.4 us (0 <= iters <= 30000) and ends: work queued on streams that
+ * share the held stream's hardware queue waits behind it, which is how the
+ * plane keeps its copy, restore and hash streams on queues of their own. */
+int kvsnap_stream_create(int device, uintptr_t* stream);
+int kvsnap_stream_destroy(uintptr_t stream);
+int kvsnap_hold_stream(uintptr_t stream, int iters);
+
 /* Seeded synthetic KV for benchmarks and tests (no reference counterpart):
  * every span of blocks [first_block, first_block + n_blocks) filled from a
  * counter-based generator keyed (seed, span, block, element); kind 0 bf16

@@ -204,6 +204,14 @@ __global__ __launch_bounds__(kRestoreThreads) void gather_to_kernel(
     }
 }
 
+// One wave that sleeps for `iters` rounds of s_sleep 127 (about 3.4 us each
+// at 2.4 GHz) and then ends: a fixed count, so every launch finishes.  The
+// data plane holds a stream with it for a few milliseconds to see which other
+// streams' work waits behind it, i.e. which streams share its hardware queue.
+__global__ __launch_bounds__(64) void hold_kernel(int iters) {
+    for (int i = 0; i < iters; ++i) __builtin_amdgcn_s_sleep(127);
+}
+
 // One workgroup per region; regions are small (one token's C elements).
 __global__ __launch_bounds__(kThreads) void zero_kernel(char* __restrict__ base, const int64_t* __restrict__ offsets,
                                                        const int64_t* __restrict__ lengths, int64_t n) {
@@ -916,6 +924,9 @@ void check_launch(const char* what) {
     if (rc != hipSuccess) throw std::runtime_error(std::string(what) + " launch: " + hipGetErrorString(rc));
 }
 
+// Longest hold: about 0.1 s at 2.4 GHz.
+constexpr int kMaxHoldIters = 30000;
+
 unsigned grid_for(int64_t jobs, int programs) {
     int64_t grid = programs > 0 ? (programs < jobs ? programs : jobs) : jobs;
     if (grid > (int64_t(1) << 30)) grid = int64_t(1) << 30;
@@ -1185,6 +1196,42 @@ int kvsnap_sha256_records(const void* records, uint64_t record_bytes, uint64_t r
                           uint8_t* out, uintptr_t stream) {
     return kvsnap_sha256_records_range(records, record_bytes, record_pitch, n_records, 0,
                                        kvsnap_sha256_blocks(record_bytes), nullptr, out, stream);
+}
+
+int kvsnap_stream_create(int device, uintptr_t* stream) {
+    return guard([&] {
+        if (!stream) throw std::runtime_error("stream create needs an output");
+        int current = 0;
+        if (hipGetDevice(&current) != hipSuccess) throw std::runtime_error("stream create: no current device");
+        if (hipSetDevice(device) != hipSuccess) throw std::runtime_error("stream create: bad device");
+        hipStream_t s = nullptr;
+        const hipError_t rc = hipStreamCreateWithFlags(&s, hipStreamNonBlocking);
+        const hipError_t back = hipSetDevice(current);
+        if (rc != hipSuccess) throw std::runtime_error(std::string("stream create: ") + hipGetErrorString(rc));
+        if (back != hipSuccess) {
+            (void)hipStreamDestroy(s);
+            throw std::runtime_error("stream create: could not restore the current device");
+        }
+        *stream = reinterpret_cast<uintptr_t>(s);
+    });
+}
+
+int kvsnap_stream_destroy(uintptr_t stream) {
+    return guard([&] {
+        if (!stream) return;
+        hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+        hipError_t rc = hipStreamSynchronize(s);
+        if (rc == hipSuccess) rc = hipStreamDestroy(s);
+        if (rc != hipSuccess) throw std::runtime_error(std::string("stream destroy: ") + hipGetErrorString(rc));
+    });
+}
+
+int kvsnap_hold_stream(uintptr_t stream, int iters) {
+    return guard([&] {
+        if (iters < 0 || iters > kMaxHoldIters) throw std::runtime_error("hold length out of range");
+        hipLaunchKernelGGL(hold_kernel, dim3(1), dim3(64), 0, reinterpret_cast<hipStream_t>(stream), iters);
+        check_launch("hold");
+    });
 }
 
 }  // extern "C"

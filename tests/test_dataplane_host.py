@@ -409,13 +409,16 @@ def test_digests_are_returned_in_block_order():
         def query(self):
             return True
 
+        def finished(self, timeout=None):
+            return True
+
         def synchronize(self):
             pass
 
     targets = targets_for("staging", 3, size)
     digests = []
     with patch.object(dataplane, "HashJob", EmulatedHashJob), \
-         patch.object(torch.Tensor, "record_stream", lambda self, stream: None):
+         patch.object(TorchBlockDataPlane, "_hash_streams", lambda self: [Mock()]):
         plane.save_gather([5, 2, 4], targets, 3 * BLOCK_SIZE - 2, digests=digests)
     result = digests[0].result()
     for i, (hexdigest, crc) in enumerate(result):

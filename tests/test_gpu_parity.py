@@ -154,6 +154,34 @@ def test_saves_and_restores_from_two_threads_overlap_byte_exact(planes):
         b.close()
 
 
+def test_restore_and_hash_streams_do_not_wait_behind_the_copy_stream(planes):
+    """The plane's own streams sit on hardware queues the copy stream does not use: while the copy stream
+    is held (one wave sleeping about 10 ms), work queued on the restore stream and on every hash stream
+    finishes.  On a shared queue it would wait out the hold."""
+    caches, _ = synth.make_caches(2, 16, layout="kv_split")
+    plane = planes(caches, restore_stream="split", restore_mode="dma")
+    lib = kernel_library()
+    copy = plane._copy_stream
+    others = [plane._restore_stream()] + list(plane._hash_streams())
+    handles = {s.cuda_stream for s in others}
+    assert len(handles) == len(others) and copy.cuda_stream not in handles
+    torch.cuda.synchronize()
+    _check(lib, lib.kvsnap_hold_stream(copy.cuda_stream, 3000))
+    held = torch.cuda.Event()
+    held.record(copy)
+    marks = []
+    for stream in others:
+        _check(lib, lib.kvsnap_hold_stream(stream.cuda_stream, 0))
+        mark = torch.cuda.Event()
+        mark.record(stream)
+        marks.append(mark)
+    for mark in marks:
+        mark.synchronize()
+    still_held = not held.query()
+    torch.cuda.synchronize()
+    assert still_held
+
+
 @pytest.mark.parametrize("layout", ["vllm", "kv_split"])
 @pytest.mark.parametrize("kind", [synth.KIND_BF16, synth.KIND_E4M3, synth.KIND_BYTES])
 def test_synthetic_fill_matches_the_oracle_generator(planes, oracle_lib, layout, kind):
