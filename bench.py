@@ -859,6 +859,155 @@ def run_cpu_roundtrip(args):
             "layout": args.layout}
 
 
+# ---------------------------------------------------------------- turn-2 time to first forward through the worker hooks
+
+def run_ttft(args):
+    """Turn 2 of a session restored through the worker hooks while an engine steps (the data plane's part
+    of the reference's bench/restore_ttft.py).
+
+    An 8k-token Qwen3-8B session is saved at turn end through ``KvsnapWorker`` into the host tier and as
+    blob files.  Then, each repetition, the engine steps a 16-sequence synthetic decode of 8k-token
+    contexts (19 GB of KV reads a step, synchronised every step as sampling does); the request arrives,
+    its load starts after that step's forward, and it runs in the first forward after the worker reports
+    it.  Time to first forward: from the arrival to the end of that forward, which reads every restored
+    block and must fold them to the checksums the saved blocks gave.  With early report the request is
+    reported once at most 128 MiB of its copy is left and the forward waits on the GPU for the rest; the
+    reference's TTFT also holds the gateway, lease and model prefill, which are not here.
+    """
+    import torch
+    from kvsnap_amd import synth
+    from kvsnap_amd.blobs import BlobDirectory
+    from kvsnap_amd.dataplane import TorchBlockDataPlane, _check, kernel_library
+    from kvsnap_amd.host_tier import HostTier
+    from kvsnap_amd.ordering import EARLY_REPORT_BYTES
+    from kvsnap_amd.worker import KvsnapMetadata, KvsnapWorker, Transfer
+
+    layers, num_blocks, block_size, tokens, seqs = 36, 16384, 16, 8192, 16
+    session = tokens // block_size
+    caches, backing = synth.make_caches(layers, num_blocks, block_size=block_size, layout=args.layout)
+    record = layers * 65536
+    plane = TorchBlockDataPlane(caches, block_size, 2 * session * record + (1 << 30))
+    plane.warm_up()
+    keep = synth.fill(plane, 0)
+    torch.cuda.synchronize()
+    del keep
+    size, total = plane.block_bytes, session * plane.block_bytes
+    source, target = synth.block_tables(num_blocks, session)
+    taken = set(source) | set(target)
+    background = random.Random(3).sample([b for b in range(1, num_blocks) if b not in taken], seqs * session)
+    tables = plane._load_tables()
+    n_spans = tables[0].numel()
+    lib = kernel_library()
+    stream = torch.cuda.current_stream()
+
+    def forward(table, n_seqs, out):
+        _check(lib, lib.kvsnap_synth_decode(tables[1].data_ptr(), tables[2].data_ptr(), tables[3].data_ptr(), n_spans,
+                                            table.data_ptr(), n_seqs, session, out.data_ptr(), 0, stream.cuda_stream))
+
+    batch = torch.tensor(background, dtype=torch.int64, device="cuda")
+    batch_out = torch.empty(seqs * n_spans, dtype=torch.int32, device="cuda")
+    src_table = torch.tensor(source, dtype=torch.int64, device="cuda")
+    dst_table = torch.tensor(target, dtype=torch.int64, device="cuda")
+    expected = torch.empty(n_spans, dtype=torch.int32, device="cuda")
+    got = torch.empty(n_spans, dtype=torch.int32, device="cuda")
+    forward(src_table, 1, expected)
+    step_ms = []
+    for _ in range(5):
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record()
+        forward(batch, seqs, batch_out)
+        end.record()
+        end.synchronize()
+        step_ms.append(start.elapsed_time(end))
+
+    root = args.disk_dir or tempfile.mkdtemp(prefix="kvsnap-ttft-")
+    tier = HostTier(plane, 2 * total)
+    worker = KvsnapWorker(plane, host_tier=tier, blobs=BlobDirectory(root))
+
+    def until(condition, seconds=60):
+        deadline = time.perf_counter() + seconds
+        while not condition():
+            if time.perf_counter() > deadline:
+                raise RuntimeError("the worker did not report in time")
+            worker.bind_connector_metadata(KvsnapMetadata())
+            worker.get_finished(set())
+            time.sleep(1e-4)
+
+    # Turn end: both saves handed off after the step's kernels, fenced, hashed on the GPU, kept.
+    worker.bind_connector_metadata(KvsnapMetadata(saves=[
+        Transfer("host", source, durability="volatile", num_kv_tokens=tokens),
+        Transfer("disk", source, durability="durable", num_kv_tokens=tokens)]))
+    worker.wait_for_save()
+    saved = {}
+    until(lambda: not worker.save_jobs)
+    meta = worker.build_connector_worker_meta()
+    if meta.errors:
+        raise RuntimeError(f"turn-end saves failed: {meta.errors}")
+    saved.update(meta.prepared)
+
+    # (snapshot, durability, check, early report, how the plane's restores cross the link)
+    arms = [("host", "volatile", "none", True, "kernel"), ("host", "volatile", "none", False, "kernel"),
+            ("host", "volatile", "none", True, "dma"), ("host", "volatile", "gpu", True, "kernel"),
+            ("disk", "durable", "gpu", True, "kernel")]
+    results, exact = {}, True
+    for name, durability, verify, early, mode in arms:
+        worker.verify = verify
+        worker.early_report_bytes = EARLY_REPORT_BYTES if early else -1
+        plane.restore_mode = mode
+        times, steps, step_times = [], [], []
+        for rep in range(args.reps + 1):               # the first repetition warms the arm up
+            if args.layout == "kv_split":              # [layers, 2, blocks, ...]
+                backing[:, :, dst_table] = 0
+            else:                                      # [layers, blocks, ...]
+                backing[:, dst_table] = 0
+            torch.cuda.synchronize()
+            arrival = time.perf_counter()
+            runnable, step, marks = False, 0, [arrival]
+            while True:
+                loads = [Transfer("r", target, snapshot=saved[name], durability=durability)] if step == 0 else []
+                worker.bind_connector_metadata(KvsnapMetadata(loads=loads))
+                forward(batch, seqs, batch_out)
+                if runnable:
+                    forward(dst_table, 1, got)
+                    torch.cuda.current_stream().synchronize()
+                    elapsed = (time.perf_counter() - arrival) * 1e3
+                    break
+                if loads:
+                    worker.start_load_kv()             # async loads start after the forward
+                torch.cuda.current_stream().synchronize()
+                marks.append(time.perf_counter())
+                runnable = "r" in worker.get_finished(set())[1]
+                step += 1
+            until(lambda: not worker.load_jobs)
+            loaded = worker.build_connector_worker_meta()
+            exact = exact and loaded.failed_loads == [] and torch.equal(got, expected)
+            if rep:
+                times.append(elapsed)
+                steps.append(step)
+                step_times.extend((b - a) * 1e3 for a, b in zip(marks, marks[1:]))
+        results[f"{name}-verify-{verify}-{'early' if early else 'at-completion'}-{mode}"] = {
+            "median_ms": round(statistics.median(times), 2), "min_ms": round(min(times), 2),
+            "max_ms": round(max(times), 2), "steps_before_forward": statistics.median(steps),
+            "engine_step_ms_while_loading": round(statistics.median(step_times), 2)}
+        log(list(results)[-1], results[list(results)[-1]])
+    worker.shutdown()
+    tier_stats = tier.stats()
+    plane.close()
+    if not args.disk_dir:
+        import shutil
+        shutil.rmtree(root, ignore_errors=True)
+    best = results["host-verify-none-early-kernel"]
+    return {"metric": "turn-2 time to first forward of an 8k-token Qwen3-8B session restored through the worker "
+                      "hooks beside a 16-sequence decode (data-plane part of TTFT)",
+            "workload": "ttft", "value": best["median_ms"], "unit": "ms", "higher_is_better": False,
+            "arms": results, "engine_step_ms": round(statistics.median(step_ms), 3), "snapshot_bytes": total,
+            "reps": args.reps, "host_tier": tier_stats, "forward_reads_restored_bytes_exact": exact,
+            "note": "arrival -> end of the first forward that reads the restored blocks; early = reported once "
+                    "<= 128 MiB is left, the forward waiting on the GPU for the rest; kernel = the restore kernel "
+                    "reads pinned memory in place (CUs beside the decode), dma = the copy engines stage each chunk "
+                    "and the scatter kernel places it; verify gpu = CRC32C checked on the GPU before any KV write"}
+
+
 # ---------------------------------------------------------------- multi-turn host-tier saves
 
 def run_turns(args):
@@ -976,8 +1125,8 @@ def main():
     parser.add_argument("--warmup", type=int, default=3)
     parser.add_argument("--layout", choices=("kv_split", "vllm"), default="kv_split")
     parser.add_argument("--workload", choices=("save-restore", "disk-fork", "rotating-fp8", "turns", "cpu-roundtrip",
-                                               "kernels", "duplex"), default="save-restore")
-    parser.add_argument("--reps", type=int, default=5, help="kernels: timed repetitions per kernel")
+                                               "kernels", "duplex", "ttft"), default="save-restore")
+    parser.add_argument("--reps", type=int, default=5, help="kernels, ttft: timed repetitions per kernel / arm")
     parser.add_argument("--kv-heads", type=int, default=8, choices=(1, 2, 4, 8),
                         help="kernels: KV heads in the cache, 8 / TP for one tensor-parallel rank's shard")
     parser.add_argument("--hash-depth", type=int, default=2,
@@ -996,7 +1145,7 @@ def main():
                         help="duplex: saves without GPU CRC32C / SHA-256 (the link alone)")
     parser.add_argument("--restore-mode", choices=("kernel", "dma"), default=None,
                         help="duplex, rotating-fp8: how restores cross the link")
-    parser.add_argument("--disk-dir", default=None, help="disk-fork, turns: where the blob files go")
+    parser.add_argument("--disk-dir", default=None, help="disk-fork, turns, ttft: where the blob files go")
     parser.add_argument("--cpu-seconds", type=float, default=20.0)
     parser.add_argument("--no-cpu-baseline", action="store_true")
     args = parser.parse_args()
@@ -1007,7 +1156,8 @@ def main():
     import torch
     torch.cuda.set_device(0)
     runner = {"save-restore": run_save_restore, "disk-fork": run_disk_fork, "rotating-fp8": run_rotating,
-              "turns": run_turns, "cpu-roundtrip": run_cpu_roundtrip, "kernels": run_kernels, "duplex": run_duplex}
+              "turns": run_turns, "cpu-roundtrip": run_cpu_roundtrip, "kernels": run_kernels, "duplex": run_duplex,
+              "ttft": run_ttft}
     print(json.dumps(runner[args.workload](args)), flush=True)
 
 

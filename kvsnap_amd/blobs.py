@@ -155,10 +155,14 @@ class BlobDirectory:
             if fenced is not None:
                 fenced.set()
             return dict(block_ids=block_ids, num_kv_tokens=num_kv_tokens, segments=segments)
+        from .dataplane import CopyFailed
         with plane.staging(len(fresh)) as staged:
             digests = []
-            plane.save_gather(fresh, [(staged, i * size) for i in range(len(fresh))], num_kv_tokens - keep * block_size,
-                              chunk_bytes=chunk_bytes, digests=digests)
+            try:
+                plane.save_gather(fresh, [(staged, i * size) for i in range(len(fresh))],
+                                  num_kv_tokens - keep * block_size, chunk_bytes=chunk_bytes, digests=digests)
+            except Exception as exc:
+                raise CopyFailed("blob save: device-to-host completion could not be proven") from exc
             if fenced is not None:
                 fenced.set()
             new = self.write_blocks([(staged.pointer + i * size, size) for i in range(len(fresh))],

@@ -27,11 +27,12 @@ mirrored here.
 """
 from __future__ import annotations
 
+from contextlib import contextmanager
 import threading
 import uuid
 
 from .blobs import CorruptSnapshotError
-from .dataplane import PinnedCapacityError
+from .dataplane import CopyFailed, PinnedCapacityError
 
 
 def unchanged_prefix(block_ids, previous, block_size):
@@ -195,8 +196,11 @@ class HostTier:
         if fresh:
             # A failure here leaves the pinned memory to the pool (the DMA may
             # still be using it), as the reference's save does (vllm.py:602-607).
-            plane.save_gather(fresh, [(allocation, 0) for allocation in allocations],
-                              num_kv_tokens - keep * block_size, chunk_bytes=chunk_bytes, digests=digests)
+            try:
+                plane.save_gather(fresh, [(allocation, 0) for allocation in allocations],
+                                  num_kv_tokens - keep * block_size, chunk_bytes=chunk_bytes, digests=digests)
+            except Exception as exc:
+                raise CopyFailed("host-tier save: device-to-host completion could not be proven") from exc
         if fenced is not None:
             fenced.set()
         ids = digests[0].result() if fresh else []
@@ -219,11 +223,30 @@ class HostTier:
         segments = snapshot["segments"]
         if len(block_ids) != len(segments):
             raise ValueError("one target block per segment is required")
+        with self.borrow(segments, snapshot["locations"]) as sources:
+            if verify:
+                self.plane.load_scatter_verified(list(block_ids), sources, [s["crc32c"] for s in segments],
+                                                 progress=progress, chunk_bytes=chunk_bytes)
+            else:
+                self.plane.load_scatter(list(block_ids), sources, progress=progress, chunk_bytes=chunk_bytes)
+        return dict(snapshot, block_ids=list(block_ids))
+
+    @contextmanager
+    def borrow(self, segments, locations):
+        """The held pinned blocks of ``segments`` as ``(allocation, 0)`` sources, held until the block exits.
+
+        Every block is checked as held (same handle, length and whole-block
+        segment) before any is lent, as ``VolatileOwner.borrow`` checks its
+        handles (reference ``volatile.py:281-314``); a block no longer held
+        raises :class:`CorruptSnapshotError` and nothing is lent.  The caller
+        must not exit the block before its copies out of the sources have
+        completed (``load_scatter`` returns after its last one).
+        """
         with self._lock:
             sources = []
             for segment in segments:
                 entry = self._entries.get(segment["blob_id"])
-                location = snapshot["locations"].get(segment["blob_id"], {})
+                location = locations.get(segment["blob_id"], {})
                 if entry is None or entry["handle"] != location.get("handle") or \
                         entry["allocation"].size != segment["length"] or segment["offset"] != 0:
                     raise CorruptSnapshotError("host-tier block no longer held")
@@ -231,11 +254,6 @@ class HostTier:
             for segment in segments:
                 self._entries[segment["blob_id"]]["refs"] += 1
         try:
-            if verify:
-                self.plane.load_scatter_verified(list(block_ids), sources, [s["crc32c"] for s in segments],
-                                                 progress=progress, chunk_bytes=chunk_bytes)
-            else:
-                self.plane.load_scatter(list(block_ids), sources, progress=progress, chunk_bytes=chunk_bytes)
+            yield sources
         finally:
             self.release(dict(segments=segments))
-        return dict(snapshot, block_ids=list(block_ids))

@@ -1,0 +1,94 @@
+"""The worker hooks on the GPU: a session saved through them into the host tier and blob files, loaded
+into other blocks, and read by the next forward on the engine stream with no host synchronisation.
+
+The forward is ordered after the copy only by what the worker does: an early-reported load's last
+event joins the next forward's waits (reference kvsnap/connector/vllm.py:454-467, 649-670).
+"""
+import random
+import time
+
+import pytest
+
+torch = pytest.importorskip("torch")
+
+from kvsnap_amd import synth
+from kvsnap_amd.blobs import BlobDirectory
+from kvsnap_amd.dataplane import TorchBlockDataPlane
+from kvsnap_amd.host_tier import HostTier
+from kvsnap_amd.worker import KvsnapMetadata, KvsnapWorker, Transfer
+
+pytestmark = pytest.mark.gpu
+
+LAYERS, BLOCKS, BLOCK_SIZE = 4, 96, 16
+
+
+def run_until(worker, condition, seconds=60):
+    """Step boundaries (bind, report) until ``condition(sending, receiving)`` holds."""
+    deadline = time.monotonic() + seconds
+    while time.monotonic() < deadline:
+        worker.bind_connector_metadata(KvsnapMetadata())
+        sending, receiving = worker.get_finished(set())
+        if condition(sending, receiving):
+            return sending, receiving
+        torch.cuda.synchronize()
+        time.sleep(1e-4)
+    raise AssertionError("the worker never reported")
+
+
+@pytest.mark.parametrize("durability", ["volatile", "durable"])
+@pytest.mark.parametrize("verify", ["gpu", "host"])
+def test_a_session_saved_and_loaded_through_the_worker_is_what_the_next_forward_reads(hip_library, tmp_path,
+                                                                                      durability, verify):
+    caches, backing = synth.make_caches(LAYERS, BLOCKS, layout="kv_split")
+    plane = TorchBlockDataPlane(caches, BLOCK_SIZE, 256 << 20)
+    plane.warm_up()
+    keep = synth.fill(plane, 3)
+    torch.cuda.synchronize()
+    del keep
+    tier = HostTier(plane, 128 << 20)
+    # The 10 MiB session is one launch: a 64 MiB threshold reports it as soon as that launch is queued.
+    worker = KvsnapWorker(plane, host_tier=tier, blobs=BlobDirectory(tmp_path), verify=verify,
+                          early_report_bytes=64 << 20)
+    try:
+        rng = random.Random(4)
+        source = rng.sample(range(1, BLOCKS), 40)
+        target = rng.sample([b for b in range(1, BLOCKS) if b not in source], 40)
+        src = torch.tensor(source, device="cuda")
+        dst = torch.tensor(target, device="cuda")
+        expected = backing[:, :, src].clone()
+        tokens = 40 * BLOCK_SIZE - 5           # a partial last block: its tail is zeroed in the snapshot
+
+        # Turn end: the save is handed off after this step's kernels, fenced, then prepared.
+        worker.bind_connector_metadata(KvsnapMetadata(saves=[Transfer("r", source, durability=durability,
+                                                                      num_kv_tokens=tokens)]))
+        worker.wait_for_save()
+        run_until(worker, lambda sending, receiving: worker.save_jobs == {})
+        meta = worker.build_connector_worker_meta()
+        assert meta.errors == {}
+        snapshot = meta.prepared["r"]
+        assert len(snapshot["segments"]) == 40
+
+        # The next turn: load into other blocks; the forward that reads them runs as soon as the
+        # load is reported, ordered after the copy on the GPU by the worker's forward waits.
+        backing[:, :, dst] = 0
+        worker.bind_connector_metadata(KvsnapMetadata(loads=[Transfer("r", target, snapshot=snapshot,
+                                                                      durability=durability)]))
+        worker.start_load_kv()
+        deadline = time.monotonic() + 60
+        while "r" not in worker.get_finished(set())[1]:
+            assert time.monotonic() < deadline, "the load was never reported"
+            time.sleep(50e-6)
+        worker.bind_connector_metadata(KvsnapMetadata())      # the forward's waits
+        restored = backing[:, :, dst].clone()                  # the forward, on the engine stream
+        torch.cuda.synchronize()
+        # The snapshot's last block carries zeros past the computed tokens.
+        expected[:, :, -1, 16 - 5:] = 0
+        assert torch.equal(restored.view(torch.int16), expected.view(torch.int16))
+        run_until(worker, lambda sending, receiving: worker.load_jobs == {})
+        loaded = worker.build_connector_worker_meta()
+        assert loaded.loaded == ["r"] and loaded.failed_loads == []
+        assert worker.get_block_ids_with_load_errors() == set()
+    finally:
+        worker.shutdown()
+        torch.cuda.synchronize()
+        plane.close()
