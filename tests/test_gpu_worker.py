@@ -88,6 +88,19 @@ def test_a_session_saved_and_loaded_through_the_worker_is_what_the_next_forward_
         loaded = worker.build_connector_worker_meta()
         assert loaded.loaded == ["r"] and loaded.failed_loads == []
         assert worker.get_block_ids_with_load_errors() == set()
+
+        # Prefix caching: the first three blocks are already in the cache and are not copied.
+        backing[:, :, dst] = 0
+        backing[:, :, dst[:3]] = 1
+        worker.bind_connector_metadata(KvsnapMetadata(loads=[Transfer("p", target, snapshot=snapshot,
+                                                                      durability=durability, skip_blocks=3)]))
+        worker.start_load_kv()
+        run_until(worker, lambda sending, receiving: "p" in receiving)
+        torch.cuda.synchronize()
+        assert bool((backing[:, :, dst[:3]] == 1).all())
+        assert torch.equal(backing[:, :, dst[3:]].view(torch.int16), expected[:, :, 3:].view(torch.int16))
+        run_until(worker, lambda sending, receiving: worker.load_jobs == {})
+        assert worker.build_connector_worker_meta().failed_loads == []
     finally:
         worker.shutdown()
         torch.cuda.synchronize()
