@@ -93,6 +93,17 @@ class KvsnapWorkerMetadata:
     loaded: list = field(default_factory=list)             # requests whose load is over
 
 
+def _caused_by(exc, kind):
+    """Whether ``exc`` or any exception it was raised from or while handling is a ``kind``."""
+    seen = set()
+    while exc is not None and id(exc) not in seen:
+        if isinstance(exc, kind):
+            return True
+        seen.add(id(exc))
+        exc = exc.__cause__ or exc.__context__
+    return False
+
+
 def _completed(fn, *args):
     """Run ``fn`` now; its outcome as a finished future (the synchronous path)."""
     future = Future()
@@ -242,10 +253,12 @@ class KvsnapWorker:
                 raise ValueError("no blob directory for a durable save")
             return self.blobs.save(self.dataplane, transfer.block_ids, transfer.num_kv_tokens,
                                    previous=transfer.previous, fenced=fenced)
-        except CopyFailed as exc:
-            # The DMA may still use the GPU blocks and the pinned memory: fenced stays unset.
-            raise DMAUnknown("kvsnap D2H completion could not be proven") from exc
-        except BaseException:
+        except BaseException as exc:
+            if _caused_by(exc, CopyFailed):
+                # The DMA may still use the GPU blocks and the pinned memory: fenced stays unset.  (A
+                # staging buffer released while its copy is unproven raises again on the way out, so
+                # the copy failure can be the context of the exception that arrives here.)
+                raise DMAUnknown("kvsnap D2H completion could not be proven") from exc
             fenced.set()    # failed before the copy started (or after it landed): the blocks may go
             raise
 
