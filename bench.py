@@ -61,6 +61,8 @@ import threading
 import time
 
 HBM_PEAK_GBPS = 8000.0
+# MI355X's host link, PCIe 5.0 x16: 32 GT/s x 16 lanes, 128b/130b encoding, per direction.
+PCIE5_X16_GBPS = round(32 * 16 * 128 / 130 / 8, 2)
 # SHA-256 runs one dependency chain per record (two lanes of a round wave).
 # The round wave issues 648 VALU per 64-byte block (counted in the gfx950 ISA
 # of sha256_kernel: 192 alignbit, 192 bitop3, 127 DPP adds, 65 add3, 64 xad,
@@ -346,6 +348,9 @@ def run_save_restore(args):
         "d2h_peak_gbps": round(d2h_peak, 2),
         "restore_frac_of_h2d": round(total / lat["restore"] / 1e6 / h2d_peak, 4),
         "save_frac_of_d2h": round(total / lat["save"] / 1e6 / d2h_peak, 4),
+        "pcie5_x16_gbps": PCIE5_X16_GBPS,
+        "restore_frac_of_pcie5_x16": round(total / lat["restore"] / 1e6 / PCIE5_X16_GBPS, 4),
+        "save_frac_of_pcie5_x16": round(total / lat["save"] / 1e6 / PCIE5_X16_GBPS, 4),
         "kernels_ms": {name: round(k["avg_ms"], 4) for name, k in kernels.items()},
         "roofline": {"kernel": "gather_kernel", "bound": "hbm", "achieved": round(gather_achieved, 1),
                      "peak": HBM_PEAK_GBPS, "unit": "GB/s", "frac": round(gather_achieved / HBM_PEAK_GBPS, 4),
