@@ -696,7 +696,7 @@ def run_duplex(args):
             "value": round(2 * total / (ms_per_step * 1e6), 3), "unit": "GB/s", "steps": args.steps,
             "warmup": args.warmup, "ms_per_step": round(ms_per_step, 3), "snapshot_bytes": total,
             "duplex_link_gbps": round(max(duplex), 2), "layout": args.layout, "restore_mode": plane.restore_mode,
-            "save_mode": plane.save_mode,
+            "save_mode": plane.save_mode, "restore_stream_check": plane.restore_stream_check,
             "parity": {"restore_byte_exact": exact, "digests_bit_exact": digests_exact},
             "note": "session k restored while session k + 1 is saved (two host threads, two pinned buffers); "
                     "each step still saves 1.208 GB with CRC32C + SHA-256 and restores 1.208 GB"}

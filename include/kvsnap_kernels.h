@@ -81,6 +81,12 @@ int kvsnap_scatter_blocks(const void* records, int64_t record_pitch, const int64
  * pinned memory in place, kvsnap/connector/copy_kernel.py:22-40). */
 int kvsnap_copy_to_device(void* dst, const void* src, size_t nbytes, uintptr_t stream);
 
+/* Copy nbytes from device memory to pinned host memory on `stream` (the DMA
+ * engines, hipMemcpyAsync); no reference counterpart.  With
+ * kvsnap_copy_to_device, the plane times which copy engine a new restore
+ * stream took (the pool's own device-to-host copies are kvsnap_pool_copy). */
+int kvsnap_copy_to_host(void* dst, const void* src, size_t nbytes, uintptr_t stream);
+
 /* Zero n byte ranges [base + offsets[i], + lengths[i]): the token slots past
  * the last computed token of a record.  Replaces the host memsets of
  * TorchBlockDataPlane._zero_tail, kvsnap/connector/dataplane.py:262-272. */

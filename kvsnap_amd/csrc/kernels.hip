@@ -1096,6 +1096,16 @@ int kvsnap_copy_to_device(void* dst, const void* src, size_t nbytes, uintptr_t s
     });
 }
 
+int kvsnap_copy_to_host(void* dst, const void* src, size_t nbytes, uintptr_t stream) {
+    return guard([&] {
+        if (nbytes == 0) return;
+        if (!dst || !src) throw std::runtime_error("copy needs a pinned destination and a device source");
+        const hipError_t rc = hipMemcpyAsync(dst, src, nbytes, hipMemcpyDeviceToHost,
+                                             reinterpret_cast<hipStream_t>(stream));
+        if (rc != hipSuccess) throw std::runtime_error(std::string("copy to host: ") + hipGetErrorString(rc));
+    });
+}
+
 int kvsnap_zero_regions(void* base, const int64_t* offsets, const int64_t* lengths, int64_t n, uintptr_t stream) {
     return guard([&] {
         if (n < 0) throw std::runtime_error("negative region count");

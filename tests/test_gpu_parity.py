@@ -154,6 +154,41 @@ def test_saves_and_restores_from_two_threads_overlap_byte_exact(planes):
         b.close()
 
 
+def test_a_copy_engine_restore_stream_shares_the_link_with_the_copy_stream(planes):
+    """With restores on their own stream through the copy engines, a restore's host-to-device copy and a
+    save's device-to-host copy share the link instead of taking turns: the plane gives its restore stream
+    another copy engine than the copy stream's at warm-up.  Streams on one engine copy in turn (the pair
+    takes the sum of the two copies' times); on two engines the pair takes about as long as the longer
+    copy."""
+    import time
+    caches, _ = synth.make_caches(2, 16, layout="kv_split")
+    plane = planes(caches, restore_stream="split", restore_mode="dma")
+    restore = plane._restore_stream()
+    assert restore is not plane._copy_stream
+    assert plane.restore_stream_check["accepted"], plane.restore_stream_check
+    lib = kernel_library()
+    nbytes = 256 << 20
+    host = torch.empty(2 * nbytes, dtype=torch.uint8, pin_memory=True)
+    dev = torch.empty(2 * nbytes, dtype=torch.uint8, device="cuda")
+
+    def timed(up, down):
+        best = float("inf")
+        for _ in range(3):
+            torch.cuda.synchronize()
+            start = time.perf_counter()
+            if up:
+                _check(lib, lib.kvsnap_copy_to_device(dev.data_ptr(), host.data_ptr(), nbytes, restore.cuda_stream))
+            if down:
+                _check(lib, lib.kvsnap_copy_to_host(host.data_ptr() + nbytes, dev.data_ptr() + nbytes, nbytes,
+                                                    plane._copy_stream.cuda_stream))
+            torch.cuda.synchronize()
+            best = min(best, time.perf_counter() - start)
+        return best
+
+    up, down, both = timed(True, False), timed(False, True), timed(True, True)
+    assert both < 0.8 * (up + down), (up, down, both)
+
+
 def test_restore_and_hash_streams_do_not_wait_behind_the_copy_stream(planes):
     """The plane's own streams sit on hardware queues the copy stream does not use: while the copy stream
     is held (one wave sleeping about 10 ms), work queued on the restore stream and on every hash stream
