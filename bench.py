@@ -221,10 +221,12 @@ def run_save_restore(args):
 
     # Latency, one operation at a time (not the timed region): save until the
     # D2H fence, save until its CRC32C and SHA-256 are ready, restore, and the
-    # restore's early-readiness point.
+    # restore's early-readiness point.  Medians of five (all five reported): in
+    # the second and later processes on a box, one restore launch of the third
+    # sample has stalled for 17-44 ms.
     latency = {"save": [], "hashed": [], "restore": [], "early": []}
     lat_timer = KernelTimer()
-    for i in range(3):
+    for i in range(6):
         plane.timer = lat_timer if i else None
         digests, progress = [], []
         t0 = time.perf_counter()
@@ -344,6 +346,7 @@ def run_save_restore(args):
         "restore_gbps": round(total / lat["restore"] / 1e6, 2),
         "restore_launches": launches,
         "restore_early_ready_ms": round(lat["early"], 3),
+        "latency_samples_ms": {k: [round(v, 2) for v in vs] for k, vs in latency.items()},
         "h2d_peak_gbps": round(h2d_peak, 2),
         "d2h_peak_gbps": round(d2h_peak, 2),
         "restore_frac_of_h2d": round(total / lat["restore"] / 1e6 / h2d_peak, 4),

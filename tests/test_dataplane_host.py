@@ -402,7 +402,7 @@ def test_digests_are_returned_in_block_order():
         """The oracle in place of the GPU hash job, with its interface."""
 
         def __init__(self, torch_module, records_ptr, record_bytes, record_pitch, n, device, stream, slice_blocks, *,
-                     timer=None, keepalive=None):
+                     timer=None, keepalive=None, executor=None):
             crcs, shas = oracle.digest_records(records_ptr, record_bytes, record_pitch, n)
             self.crc, self.sha = torch.from_numpy(crcs.astype(np.int64)), torch.from_numpy(shas)
 
