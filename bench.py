@@ -220,11 +220,13 @@ def run_save_restore(args):
     log(f"DMA peaks: H2D {h2d_peak:.1f} GB/s, D2H {d2h_peak:.1f} GB/s")
 
     # Latency, one operation at a time (not the timed region): save until the
-    # D2H fence, save until its CRC32C and SHA-256 are ready, restore, and the
-    # restore's early-readiness point.  Medians of five (all five reported): in
+    # D2H fence, save until its CRC32C and SHA-256 are ready, restore, the
+    # restore's early-readiness point, and the checked restore (every block's
+    # CRC32C folded in as it is copied, then compared with the save's).
+    # Medians of five (all five reported): in
     # the second and later processes on a box, one restore launch of the third
     # sample has stalled for 17-44 ms.
-    latency = {"save": [], "hashed": [], "restore": [], "early": []}
+    latency = {"save": [], "hashed": [], "restore": [], "early": [], "checked": []}
     lat_timer = KernelTimer()
     for i in range(6):
         plane.timer = lat_timer if i else None
@@ -232,11 +234,14 @@ def run_save_restore(args):
         t0 = time.perf_counter()
         plane.save_gather(source, targets, tokens, digests=digests)
         t1 = time.perf_counter()
-        digests[0].result()
+        saved_crcs = [crc for _, crc in digests[0].result()]
         t2 = time.perf_counter()
         plane.load_scatter(target, targets, progress=progress)
         t3 = time.perf_counter()
+        plane.load_scatter_checked(target, targets, saved_crcs)
+        t4 = time.perf_counter()
         if i:
+            latency["checked"].append((t4 - t3) * 1e3)
             latency["save"].append((t1 - t0) * 1e3)
             latency["hashed"].append((t2 - t0) * 1e3)
             latency["restore"].append((t3 - t2) * 1e3)
@@ -245,6 +250,7 @@ def run_save_restore(args):
             latency["early"].append(pairs[0][0].elapsed_time(pairs[early_launch_index(progress)][1]))
     plane.timer = None
     lat = {k: statistics.median(v) for k, v in latency.items()}
+    checked_launch_ms = lat_timer.summary()["restore_checked"]["avg_ms"]
 
     # Throughput: each step saves the session (gather, D2H, GPU CRC32C +
     # SHA-256) and restores it into the target blocks.  A save's digests are
@@ -346,6 +352,10 @@ def run_save_restore(args):
         "restore_gbps": round(total / lat["restore"] / 1e6, 2),
         "restore_launches": launches,
         "restore_early_ready_ms": round(lat["early"], 3),
+        "restore_checked_ms": round(lat["checked"], 3),
+        "restore_checked_gbps": round(total / lat["checked"] / 1e6, 2),
+        "restore_checked_frac_of_h2d": round(total / lat["checked"] / 1e6 / h2d_peak, 4),
+        "restore_checked_launch_ms": round(checked_launch_ms, 4),
         "latency_samples_ms": {k: [round(v, 2) for v in vs] for k, vs in latency.items()},
         "h2d_peak_gbps": round(h2d_peak, 2),
         "d2h_peak_gbps": round(d2h_peak, 2),

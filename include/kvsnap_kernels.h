@@ -45,6 +45,29 @@ int kvsnap_restore_blocks(const int64_t* sources, const int64_t* blocks, int64_t
                           const int64_t* span_words, int64_t n_spans, int64_t min_span_bytes, int programs,
                           uintptr_t stream);
 
+/* Checked restore: the copy of kvsnap_restore_blocks (any span length and
+ * 8-byte alignment), and partial[i * n_spans + s] = the raw CRC32C (zero
+ * initial value, no final xor) of block i's span s at the span's end, folded
+ * from the bytes as they are copied.  kvsnap_restore_checked_crc32c then
+ * gives each block's CRC32C from its partials.  Replaces the host
+ * CRC32C checks that precede a restore from pinned memory:
+ * VolatileOwner.borrow(verify_checksums=True), kvsnap/connector/volatile.py:
+ * 302-305, and the staged fetch's check at kvsnap/connector/vllm.py:531
+ * (kvsnap_crc32c_extend, csrc/dataplane/io.cpp:39-44), each of which reads
+ * the block once more on the host before the copy. */
+int kvsnap_restore_blocks_checked(const int64_t* sources, const int64_t* blocks, int64_t n_blocks,
+                                  const int64_t* span_offsets, const int64_t* span_bases, const int64_t* span_pitches,
+                                  const int64_t* span_words, int64_t n_spans, int programs, uint32_t* partial,
+                                  uintptr_t stream);
+
+/* out[i] = CRC32C (init/xorout ~0) of the record_bytes of block i whose spans
+ * (span_offsets / span_words, the restore's tables; at most 8192 spans) tile
+ * the record, from the n_blocks * n_spans partials kvsnap_restore_blocks_checked
+ * wrote.  Bit-exact with kvsnap_crc32c_extend(record, record_bytes, 0). */
+int kvsnap_restore_checked_crc32c(const uint32_t* partial, int64_t n_blocks, const int64_t* span_offsets,
+                                  const int64_t* span_words, int64_t n_spans, uint64_t record_bytes, uint32_t* out,
+                                  uintptr_t stream);
+
 /* Gather: block blocks[i]'s spans packed into records + i * record_pitch.
  * Replaces save_gather's torch.cat([raw.index_select(0, ids) ...], out=stage),
  * kvsnap/connector/dataplane.py:416-417. */

@@ -554,6 +554,165 @@ __global__ __launch_bounds__(64) void crc_combine_kernel(const uint32_t* __restr
     out[r] = ~(init_term ^ s);
 }
 
+// ----------------------------------------------------------------- restore with CRC32C
+//
+// The restore kernel's copy with each record's CRC32C computed from the bytes
+// on their way through, so a checked restore costs one pass over the host
+// link and none over HBM.  The host link is the bound (57 GB/s against the
+// several TB/s the LDS lookups sustain), so the tables are shared, not one
+// copy per lane as in the CRC kernel above.
+//
+// One wave per (block, span) job, jobs in the reference kernel's order.  Lane
+// l takes the 16-byte slots l, l + 64, l + 128, ... of its span and folds
+// them into acc, advancing acc by one row (64 slots, 1 KiB) per slot, so acc
+// is the raw CRC of the lane's slots with the others as zeros, at its last
+// slot.  With r = slots mod 64, that slot ends 16 * ((r - 1 - l) mod 64)
+// bytes before the last slot of the span, whichever lanes own the short last
+// row; M[k] = x^(128 k) moves it there.  A span of 8 bytes past its slots (a
+// block size that is not even) has that word copied and folded by lane 0,
+// after the others move past it by x^64.  The wave's XOR is the raw CRC of
+// the span at its end, partial[job]; the finish kernel shifts every span to
+// the end of its record.
+
+constexpr int kCheckedUnroll = 8;                 // slots per lane per pass: 8 KiB per wave, 32 KiB per workgroup
+constexpr int kCheckedAdvance = 0;                // G: advance by 1 KiB, [4][256]
+constexpr int kCheckedSlicing = 1024;             // S: slicing-by-4, [4][256]
+constexpr int kCheckedRowShift = 2048;            // M[64]: x^(128 k)
+constexpr int kCheckedLdsWords = kCheckedRowShift + 64;
+constexpr int kCheckedPowers = kCheckedLdsWords;  // x^(8 * 2^k), k < 48, read from global memory only
+constexpr int kCheckedTableWords = kCheckedPowers + 48;
+
+__device__ uint32_t g_crc_checked_tables[kCheckedTableWords];
+
+__device__ __forceinline__ uint32_t crc_dword_shared(const uint32_t* s, uint32_t x) {
+    return xor3(s[x & 0xFFu], s[256 + ((x >> 8) & 0xFFu)], s[512 + ((x >> 16) & 0xFFu)]) ^ s[768 + (x >> 24)];
+}
+
+__device__ __forceinline__ uint32_t crc_word_shared(const uint32_t* s, u32x4 v) {
+    uint32_t c = crc_dword_shared(s, v.x);
+    c = crc_dword_shared(s, c ^ v.y);
+    c = crc_dword_shared(s, c ^ v.z);
+    return crc_dword_shared(s, c ^ v.w);
+}
+
+// A 16-byte slot, as one dwordx4 access (kWide) or two 8-byte ones.
+template <bool kWide>
+__device__ __forceinline__ u32x4 load_slot(const char* p) {
+    if (kWide) return __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+    const uint64_t* q = reinterpret_cast<const uint64_t*>(p);
+    const uint64_t a = __builtin_nontemporal_load(q), b = __builtin_nontemporal_load(q + 1);
+    return u32x4{static_cast<uint32_t>(a), static_cast<uint32_t>(a >> 32), static_cast<uint32_t>(b),
+                 static_cast<uint32_t>(b >> 32)};
+}
+
+template <bool kWide>
+__device__ __forceinline__ void store_slot(char* p, u32x4 v) {
+    if (kWide) {
+        __builtin_nontemporal_store(v, reinterpret_cast<u32x4*>(p));
+        return;
+    }
+    uint64_t* q = reinterpret_cast<uint64_t*>(p);
+    __builtin_nontemporal_store(static_cast<uint64_t>(v.x) | (static_cast<uint64_t>(v.y) << 32), q);
+    __builtin_nontemporal_store(static_cast<uint64_t>(v.z) | (static_cast<uint64_t>(v.w) << 32), q + 1);
+}
+
+// Copy one span (nbytes a multiple of 8) with one wave and return this lane's
+// share of its raw CRC32C at the span's end.
+template <bool kWide>
+__device__ __forceinline__ uint32_t copy_span_crc(const char* __restrict__ src, char* __restrict__ dst,
+                                                  int64_t nbytes, int lane, const uint32_t* lds) {
+    const uint32_t* slicing = lds + kCheckedSlicing;
+    const int64_t slots = nbytes >> 4;
+    uint32_t acc = 0;
+    for (int64_t row = 0; row < slots; row += kCheckedUnroll * 64) {  // wave-uniform
+        const int64_t i = row + lane;
+        u32x4 v[kCheckedUnroll];
+        if (row + kCheckedUnroll * 64 <= slots) {
+#pragma unroll
+            for (int u = 0; u < kCheckedUnroll; ++u) v[u] = load_slot<kWide>(src + 16 * (i + u * 64));
+#pragma unroll
+            for (int u = 0; u < kCheckedUnroll; ++u) store_slot<kWide>(dst + 16 * (i + u * 64), v[u]);
+#pragma unroll
+            for (int u = 0; u < kCheckedUnroll; ++u) acc = crc_advance(lds, acc) ^ crc_word_shared(slicing, v[u]);
+        } else {
+#pragma unroll
+            for (int u = 0; u < kCheckedUnroll; ++u)
+                v[u] = i + u * 64 < slots ? load_slot<kWide>(src + 16 * (i + u * 64)) : u32x4{0u, 0u, 0u, 0u};
+#pragma unroll
+            for (int u = 0; u < kCheckedUnroll; ++u)
+                if (i + u * 64 < slots) store_slot<kWide>(dst + 16 * (i + u * 64), v[u]);
+#pragma unroll
+            for (int u = 0; u < kCheckedUnroll; ++u)
+                if (i + u * 64 < slots) acc = crc_advance(lds, acc) ^ crc_word_shared(slicing, v[u]);
+        }
+    }
+    const int r = static_cast<int>(slots & 63);
+    uint32_t x = gf_mul(lds[kCheckedRowShift + ((r - 1 - lane) & 63)], acc);
+    if (nbytes & 8) {
+        x = gf_mul(g_crc_checked_tables[kCheckedPowers + 3], x);  // past the last 8 bytes: x^64
+        if (lane == 0) {
+            const uint64_t w = *reinterpret_cast<const uint64_t*>(src + 16 * slots);
+            *reinterpret_cast<uint64_t*>(dst + 16 * slots) = w;
+            x ^= crc_dword_shared(slicing, crc_dword_shared(slicing, static_cast<uint32_t>(w)) ^
+                                               static_cast<uint32_t>(w >> 32));
+        }
+    }
+    return x;
+}
+
+__global__ __launch_bounds__(kRestoreThreads) void restore_checked_kernel(
+    const int64_t* __restrict__ sources, const int64_t* __restrict__ blocks, int64_t n_blocks,
+    const int64_t* __restrict__ offs, const int64_t* __restrict__ bases, const int64_t* __restrict__ pitches,
+    const int64_t* __restrict__ words, int64_t n_spans, uint32_t* __restrict__ partial) {
+    __shared__ uint32_t lds[kCheckedLdsWords];
+    for (int i = threadIdx.x; i < kCheckedLdsWords; i += kRestoreThreads) lds[i] = g_crc_checked_tables[i];
+    __syncthreads();
+    constexpr int kWaves = kRestoreThreads / 64;
+    const int lane = static_cast<int>(threadIdx.x) & 63;
+    const int64_t wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) >> 6);
+    const int64_t jobs = n_blocks * n_spans;
+    for (int64_t job = static_cast<int64_t>(blockIdx.x) * kWaves + wave; job < jobs;
+         job += static_cast<int64_t>(gridDim.x) * kWaves) {
+        const int64_t b = job / n_spans, s = job - b * n_spans;
+        const char* src = reinterpret_cast<const char*>(sources[b] + offs[s]);
+        char* dst = reinterpret_cast<char*>(bases[s] + blocks[b] * pitches[s]);
+        const int64_t nbytes = words[s] * 8;
+        const bool wide = ((reinterpret_cast<uintptr_t>(src) | reinterpret_cast<uintptr_t>(dst)) & 15) == 0;
+        uint32_t x = wide ? copy_span_crc<true>(src, dst, nbytes, lane, lds)
+                          : copy_span_crc<false>(src, dst, nbytes, lane, lds);
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) x ^= __shfl_xor(x, o);
+        if (lane == 0) partial[job] = x;
+    }
+}
+
+// x^(8 n) mod P from the powers x^(8 * 2^k), k < 48.
+__device__ __forceinline__ uint32_t xpow8n(uint64_t n) {
+    uint32_t result = 0x80000000u;  // x^0
+    for (int k = 0; k < 48; ++k)
+        if ((n >> k) & 1) result = gf_mul(g_crc_checked_tables[kCheckedPowers + k], result);
+    return result;
+}
+
+// Record r's CRC32C from its spans' partials: span j's raw CRC moves from the
+// span's end to the record's, x^(8 (record_bytes - offset_j - bytes_j)), and
+// the initial ~0 adds init_term.  The shifts are the workgroup's first work,
+// in dynamic LDS, one span per lane.
+__global__ __launch_bounds__(64) void restore_checked_finish_kernel(
+    const uint32_t* __restrict__ partial, int64_t n_records, const int64_t* __restrict__ offs,
+    const int64_t* __restrict__ words, int64_t n_spans, uint64_t record_bytes, uint32_t init_term,
+    uint32_t* __restrict__ out) {
+    extern __shared__ uint32_t shifts[];
+    for (int64_t j = threadIdx.x; j < n_spans; j += 64)
+        shifts[j] = xpow8n(record_bytes - static_cast<uint64_t>(offs[j]) - static_cast<uint64_t>(words[j]) * 8);
+    __syncthreads();
+    const int64_t r = static_cast<int64_t>(blockIdx.x) * 64 + threadIdx.x;
+    if (r >= n_records) return;
+    uint32_t s = 0;
+    for (int64_t j = 0; j < n_spans; ++j) s ^= gf_mul(shifts[j], partial[r * n_spans + j]);
+    out[r] = ~(init_term ^ s);
+}
+
 // ----------------------------------------------------------------- SHA-256 (FIPS 180-4)
 //
 // SHA-256 is a sequential chain of 64-byte compressions within a record, so
@@ -905,6 +1064,18 @@ void ensure_crc_tables() {
         tables[kCrcLaneShift + t] = host_xpow8n(16ull * (kCrcThreads - 1 - t));
     hipError_t rc = hipMemcpyToSymbol(HIP_SYMBOL(g_crc_tables), tables, sizeof tables, 0, hipMemcpyHostToDevice);
     if (rc != hipSuccess) throw std::runtime_error(std::string("CRC32C table upload: ") + hipGetErrorString(rc));
+    // The checked restore's: G (advance by one 1 KiB row), S (slicing-by-4), M, then x^(8 * 2^k).
+    static uint32_t checked[kCheckedTableWords];
+    const uint32_t row_shift = host_xpow8n(1024);
+    for (uint32_t k = 0; k < 4; ++k)
+        for (uint32_t v = 0; v < 256; ++v) {
+            checked[kCheckedAdvance + 256 * k + v] = host_gf_mul(row_shift, v << (8 * k));
+            checked[kCheckedSlicing + 256 * k + v] = tables[256 * k + v];
+        }
+    for (uint32_t k = 0; k < 64; ++k) checked[kCheckedRowShift + k] = host_xpow8n(16ull * k);
+    for (uint32_t k = 0; k < 48; ++k) checked[kCheckedPowers + k] = host_xpow8n(1ull << k);
+    rc = hipMemcpyToSymbol(HIP_SYMBOL(g_crc_checked_tables), checked, sizeof checked, 0, hipMemcpyHostToDevice);
+    if (rc != hipSuccess) throw std::runtime_error(std::string("CRC32C table upload: ") + hipGetErrorString(rc));
     g_tables_ready[device] = true;
 }
 
@@ -926,6 +1097,9 @@ void check_launch(const char* what) {
 
 // Longest hold: about 0.1 s at 2.4 GHz.
 constexpr int kMaxHoldIters = 30000;
+
+// The checked restore's finish keeps one shift per span in LDS.
+constexpr int64_t kMaxCheckedSpans = 8192;
 
 unsigned grid_for(int64_t jobs, int programs) {
     int64_t grid = programs > 0 ? (programs < jobs ? programs : jobs) : jobs;
@@ -1012,6 +1186,44 @@ int kvsnap_restore_blocks(const int64_t* sources, const int64_t* blocks, int64_t
                            reinterpret_cast<hipStream_t>(stream), sources, blocks, n_blocks, span_offsets,
                            span_bases, span_pitches, span_words, n_spans, shape.lane_shift);
         check_launch("restore");
+    });
+}
+
+int kvsnap_restore_blocks_checked(const int64_t* sources, const int64_t* blocks, int64_t n_blocks,
+                                  const int64_t* span_offsets, const int64_t* span_bases, const int64_t* span_pitches,
+                                  const int64_t* span_words, int64_t n_spans, int programs, uint32_t* partial,
+                                  uintptr_t stream) {
+    return guard([&] {
+        if (n_blocks < 0 || n_spans < 0) throw std::runtime_error("negative restore size");
+        if (n_blocks == 0 || n_spans == 0) return;
+        if (!sources || !blocks || !span_offsets || !span_bases || !span_pitches || !span_words || !partial)
+            throw std::runtime_error("checked restore tables and partials must be device pointers");
+        if (reinterpret_cast<uintptr_t>(partial) % 4) throw std::runtime_error("checked restore partials misaligned");
+        ensure_crc_tables();
+        constexpr int64_t waves = kRestoreThreads / 64;
+        const unsigned grid = grid_for((n_blocks * n_spans + waves - 1) / waves, programs);
+        hipLaunchKernelGGL(restore_checked_kernel, dim3(grid), dim3(kRestoreThreads), 0,
+                           reinterpret_cast<hipStream_t>(stream), sources, blocks, n_blocks, span_offsets,
+                           span_bases, span_pitches, span_words, n_spans, partial);
+        check_launch("checked restore");
+    });
+}
+
+int kvsnap_restore_checked_crc32c(const uint32_t* partial, int64_t n_blocks, const int64_t* span_offsets,
+                                  const int64_t* span_words, int64_t n_spans, uint64_t record_bytes, uint32_t* out,
+                                  uintptr_t stream) {
+    return guard([&] {
+        if (n_blocks < 0 || n_spans < 0) throw std::runtime_error("negative record count");
+        if (n_blocks == 0) return;
+        if (n_spans > kMaxCheckedSpans) throw std::runtime_error("too many spans for the checked restore");
+        if (!out || (n_spans && (!partial || !span_offsets || !span_words)))
+            throw std::runtime_error("checked restore CRC32C needs device pointers");
+        ensure_crc_tables();
+        const size_t lds = static_cast<size_t>(n_spans > 0 ? n_spans : 1) * sizeof(uint32_t);
+        hipLaunchKernelGGL(restore_checked_finish_kernel, dim3(static_cast<unsigned>((n_blocks + 63) / 64)),
+                           dim3(64), lds, reinterpret_cast<hipStream_t>(stream), partial, n_blocks, span_offsets,
+                           span_words, n_spans, record_bytes, host_shift(~0u, record_bytes), out);
+        check_launch("checked restore CRC32C");
     });
 }
 

@@ -15,11 +15,14 @@ it:
   place from the host tier (:meth:`kvsnap_amd.host_tier.HostTier.borrow`); a
   durable one's from blob files, pipelined through pinned staging and
   CRC-checked (:meth:`TorchBlockDataPlane.load_from_disk`); with
-  ``verify="gpu"`` (default) every block's CRC32C is checked on the GPU
-  before it reaches the cache, with ``"host"`` on the host cores.  A failure before
-  any copy (the scheduler's error, a block no longer held, a corrupt block)
-  is a failed load whose blocks are recomputed; a copy failure is
-  :class:`DMAUnknown`, which stops the engine.
+  ``verify="gpu"`` (default) every block's CRC32C is checked on the GPU (a
+  volatile block's as the restore kernel copies it,
+  :meth:`TorchBlockDataPlane.load_scatter_checked`; a durable block's before
+  it reaches the cache), with ``"host"`` on the host cores.  A failure before
+  any copy (the scheduler's error, a block no longer held, a corrupt block),
+  or a CRC32C mismatch found by the checked copy, is a failed load whose
+  blocks are recomputed; a copy failure is :class:`DMAUnknown`, which stops
+  the engine.  A checked load is reported once its check has passed.
 * ``wait_for_save`` / ``_save`` (``vllm.py:561-608``): saves run on two threads
   after this step's kernels; ``fenced`` is set once the D2H has landed and
   the GPU blocks may be freed, before the digests and the host-tier adoption
@@ -189,11 +192,11 @@ class KvsnapWorker:
                 ready.synchronize()
                 try:
                     if self.verify == "gpu":
-                        return plane.load_scatter_verified(targets, sources, [s["crc32c"] for s in segments],
-                                                           progress=progress)
+                        return plane.load_scatter_checked(targets, sources, [s["crc32c"] for s in segments],
+                                                          progress=progress)
                     return plane.load_scatter(targets, sources, progress=progress)
                 except CorruptSnapshotError:
-                    raise               # the verified restore refused the bytes before any KV write
+                    raise               # a block failed its CRC32C; none of them is reported loaded
                 except Exception as exc:
                     raise DMAUnknown("kvsnap H2D completion could not be proven") from exc
         if self.blobs is None:

@@ -594,6 +594,92 @@ def test_qwen3_8b_8k_session_at_full_size(planes, oracle_lib):
     staged.close()
 
 
+@pytest.mark.parametrize("layout,dtype,block_size,heads,head_dim,source_shift", [
+    ("vllm", "bf16", 16, 8, 128, 0),        # 64 KiB spans, 16-byte accesses
+    ("kv_split", "bf16", 16, 8, 128, 8),    # 32 KiB spans from sources 8 bytes off 16: 8-byte accesses
+    ("kv_split", "fp8", 16, 8, 128, 0),     # 16 KiB spans
+    ("kv_split", "bf16", 16, 1, 40, 0),     # 1280-byte spans: 80 slots, a short last row of 16
+    ("vllm", "bf16", 3, 1, 4, 0),           # 48-byte spans: 3 slots
+    ("kv_split", "bf16", 3, 1, 4, 8),       # 24-byte spans: 1 slot and an 8-byte word; blocks 8 bytes off 16
+])
+def test_the_checked_restore_kernel_gives_every_record_s_crc32c_and_the_restore_s_bytes(
+        planes, oracle_lib, layout, dtype, block_size, heads, head_dim, source_shift):
+    """kvsnap_restore_blocks_checked + kvsnap_restore_checked_crc32c through the C-ABI: the KV cache after the
+    copy equals the oracle's scatter of the same records, and every record's CRC32C equals the oracle's
+    (kvsnap_crc32c_extend, csrc/dataplane/io.cpp:39-44), over spans of every length class the kernel handles."""
+    torch_dtype = torch.bfloat16 if dtype == "bf16" else torch.float8_e4m3fn
+    caches, backing = synth.make_caches(4, 64, block_size=block_size, heads=heads, head_dim=head_dim,
+                                        dtype=torch_dtype, layout=layout)
+    raw = backing.view(torch.uint8)
+    generator = torch.Generator(device="cuda").manual_seed(5)
+    raw.copy_(torch.randint(0, 256, raw.shape, dtype=torch.uint8, device="cuda", generator=generator))
+    plane = planes(caches, block_size=block_size)
+    size, n = plane.block_bytes, 29
+    staging = plane.pool.reserve(n * size + 16)
+    records = np.random.default_rng(6).integers(0, 256, n * size, dtype=np.uint8)
+    C.memmove(staging.pointer + source_shift, records.ctypes.data, n * size)
+    addresses = [staging.pointer + source_shift + i * size for i in range(n)]
+    targets = random.Random(7).sample(range(64), n)
+    expected = host_copy(backing)
+    oracle_lib.scatter(host_spans(plane, backing, expected), targets, addresses)
+    crcs = [oracle_lib.crc32c_at(address, size) for address in addresses]
+
+    tables = plane._load_tables()
+    n_spans = tables[0].numel()
+    lib = kernel_library()
+    table = torch.tensor(addresses + targets, dtype=torch.int64, device="cuda")
+    partial = torch.full((n * n_spans,), -1, dtype=torch.int32, device="cuda")
+    out = torch.zeros(n, dtype=torch.int32, device="cuda")
+    stream = torch.cuda.current_stream().cuda_stream
+    for first, last in ((0, 17), (17, n)):      # two launches, each writing its blocks' partials
+        _check(lib, lib.kvsnap_restore_blocks_checked(
+            table.data_ptr() + 8 * first, table.data_ptr() + 8 * (n + first), last - first,
+            *(t.data_ptr() for t in tables), n_spans, 64, partial.data_ptr() + 4 * first * n_spans, stream))
+    _check(lib, lib.kvsnap_restore_checked_crc32c(partial.data_ptr(), n, tables[0].data_ptr(), tables[3].data_ptr(),
+                                                  n_spans, size, out.data_ptr(), stream))
+    torch.cuda.synchronize()
+    assert [value & 0xFFFFFFFF for value in out.tolist()] == crcs
+    assert np.array_equal(host_copy(backing), expected)
+    staging.close()
+
+
+@pytest.mark.parametrize("restore_mode", ["kernel", "dma"])
+def test_a_checked_restore_loads_clean_blocks_and_reports_a_corrupt_one_only_after_the_copy(planes, oracle_lib,
+                                                                                           restore_mode):
+    from kvsnap_amd.blobs import CorruptSnapshotError
+    caches, backing = synth.make_caches(LAYERS, 40, layout="kv_split")
+    plane = planes(caches, restore_mode=restore_mode)
+    keep = synth.fill(plane, 23)
+    torch.cuda.synchronize()
+    del keep
+    saved, restored = synth.block_tables(40, 12)
+    size = plane.block_bytes
+    staged = plane.pool.reserve(12 * size)
+    sources = [(staged, i * size) for i in range(12)]
+    digests = []
+    plane.save_gather(saved, sources, 12 * BLOCK_SIZE, digests=digests)
+    crcs = [crc for _, crc in digests[0].result()]
+    before = host_copy(backing)
+    expected = before.copy()
+    oracle_lib.scatter(host_spans(plane, backing, expected), restored, [staged.pointer + i * size for i in range(12)])
+    # One flipped bit in the tenth block: the copy completes, the load is refused and nothing is reported.
+    flip = staged.pointer + 9 * size + 4321
+    C.memmove(flip, bytes([C.string_at(flip, 1)[0] ^ 16]), 1)
+    progress = []
+    with pytest.raises(CorruptSnapshotError, match=r"1 of 12 .*block 9\)"):
+        plane.load_scatter_checked(restored, sources, crcs, progress=progress)
+    assert progress == []
+    torch.cuda.synchronize()
+    corrupt = expected.copy()
+    oracle_lib.scatter(host_spans(plane, backing, corrupt), restored, [staged.pointer + i * size for i in range(12)])
+    assert np.array_equal(host_copy(backing), corrupt)
+    C.memmove(flip, bytes([C.string_at(flip, 1)[0] ^ 16]), 1)
+    assert plane.load_scatter_checked(restored, sources, crcs, progress=progress, chunk_bytes=5 * size) == 3
+    assert [left for _, left in progress] == [12 * size, 0] and progress[1][0].query()
+    assert np.array_equal(host_copy(backing), expected)
+    staged.close()
+
+
 @pytest.mark.parametrize("layout", ["kv_split", "vllm"])
 @pytest.mark.parametrize("restore_mode", ["kernel", "dma"])
 def test_a_tensor_parallel_shard_round_trips_with_short_spans(planes, oracle_lib, layout, restore_mode):
