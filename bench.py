@@ -1023,7 +1023,9 @@ def run_ttft(args):
             "note": "arrival -> end of the first forward that reads the restored blocks; early = reported once "
                     "<= 128 MiB is left, the forward waiting on the GPU for the rest; kernel = the restore kernel "
                     "reads pinned memory in place (CUs beside the decode), dma = the copy engines stage each chunk "
-                    "and the scatter kernel places it; verify gpu = CRC32C checked on the GPU before any KV write"}
+                    "and the scatter kernel places it; verify gpu = every block's CRC32C checked on the GPU: host-tier "
+                    "blocks by the restore kernel as it copies them (the load reported once the check has passed), "
+                    "disk blocks in device staging before any KV write"}
 
 
 # ---------------------------------------------------------------- multi-turn host-tier saves
