@@ -966,7 +966,7 @@ def run_ttft(args):
     # (snapshot, durability, check, early report, how the plane's restores cross the link)
     arms = [("host", "volatile", "none", True, "kernel"), ("host", "volatile", "none", False, "kernel"),
             ("host", "volatile", "none", True, "dma"), ("host", "volatile", "gpu", True, "kernel"),
-            ("disk", "durable", "gpu", True, "kernel")]
+            ("host", "volatile", "gpu", True, "dma"), ("disk", "durable", "gpu", True, "kernel")]
     results, exact = {}, True
     for name, durability, verify, early, mode in arms:
         worker.verify = verify
@@ -1024,7 +1024,8 @@ def run_ttft(args):
                     "<= 128 MiB is left, the forward waiting on the GPU for the rest; kernel = the restore kernel "
                     "reads pinned memory in place (CUs beside the decode), dma = the copy engines stage each chunk "
                     "and the scatter kernel places it; verify gpu = every block's CRC32C checked on the GPU: host-tier "
-                    "blocks by the restore kernel as it copies them (the load reported once the check has passed), "
+                    "blocks by the checked restore kernel as it copies them from pinned memory (kernel) or places "
+                    "each staged chunk (dma), the load reported once the check has passed; "
                     "disk blocks in device staging before any KV write"}
 
 
