@@ -594,21 +594,22 @@ def test_qwen3_8b_8k_session_at_full_size(planes, oracle_lib):
     staged.close()
 
 
-@pytest.mark.parametrize("layout,dtype,block_size,heads,head_dim,source_shift", [
-    ("vllm", "bf16", 16, 8, 128, 0),        # 64 KiB spans, 16-byte accesses
-    ("kv_split", "bf16", 16, 8, 128, 8),    # 32 KiB spans from sources 8 bytes off 16: 8-byte accesses
-    ("kv_split", "fp8", 16, 8, 128, 0),     # 16 KiB spans
-    ("kv_split", "bf16", 16, 1, 40, 0),     # 1280-byte spans: 80 slots, a short last row of 16
-    ("vllm", "bf16", 3, 1, 4, 0),           # 48-byte spans: 3 slots
-    ("kv_split", "bf16", 3, 1, 4, 8),       # 24-byte spans: 1 slot and an 8-byte word; blocks 8 bytes off 16
+@pytest.mark.parametrize("layers,layout,dtype,block_size,heads,head_dim,source_shift", [
+    (4, "vllm", "bf16", 16, 8, 128, 0),        # 64 KiB spans, 16-byte accesses
+    (4, "kv_split", "bf16", 16, 8, 128, 8),    # 32 KiB spans from sources 8 bytes off 16: 8-byte accesses
+    (4, "kv_split", "fp8", 16, 8, 128, 0),     # 16 KiB spans
+    (4, "kv_split", "bf16", 16, 1, 40, 0),     # 1280-byte spans: 80 slots, a short last row of 16
+    (4, "vllm", "bf16", 3, 1, 4, 0),           # 48-byte spans: 3 slots
+    (4, "kv_split", "bf16", 3, 1, 4, 8),       # 24-byte spans: 1 slot and an 8-byte word; blocks 8 bytes off 16
+    (36, "kv_split", "bf16", 16, 1, 128, 0),   # a TP = 8 shard of Qwen3-8B: 72 spans of 4 KiB per record
 ])
 def test_the_checked_restore_kernel_gives_every_record_s_crc32c_and_the_restore_s_bytes(
-        planes, oracle_lib, layout, dtype, block_size, heads, head_dim, source_shift):
+        planes, oracle_lib, layers, layout, dtype, block_size, heads, head_dim, source_shift):
     """kvsnap_restore_blocks_checked + kvsnap_restore_checked_crc32c through the C-ABI: the KV cache after the
     copy equals the oracle's scatter of the same records, and every record's CRC32C equals the oracle's
     (kvsnap_crc32c_extend, csrc/dataplane/io.cpp:39-44), over spans of every length class the kernel handles."""
     torch_dtype = torch.bfloat16 if dtype == "bf16" else torch.float8_e4m3fn
-    caches, backing = synth.make_caches(4, 64, block_size=block_size, heads=heads, head_dim=head_dim,
+    caches, backing = synth.make_caches(layers, 64, block_size=block_size, heads=heads, head_dim=head_dim,
                                         dtype=torch_dtype, layout=layout)
     raw = backing.view(torch.uint8)
     generator = torch.Generator(device="cuda").manual_seed(5)
