@@ -275,7 +275,9 @@ def run_save_restore(args):
     for _ in range(args.warmup):
         step()
     drain()
-    timer = KernelTimer()
+    # In the timed steps only the roofline's kernel, the gather (one launch a step), carries timing events:
+    # a pair around each of a step's ~50 launches added about 0.15 ms of stream time per step.
+    timer = KernelTimer(names={"gather"})
     plane.timer = timer
     torch.cuda.synchronize()
     start = time.perf_counter()
@@ -285,9 +287,16 @@ def run_save_restore(args):
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - start
     plane.timer = None
-    kernels = timer.summary()
     ms_per_step = elapsed * 1e3 / args.steps
-    launches = kernels["restore"]["launches"] // args.steps
+    # The other kernels' in-step times: a few more steps, every launch timed, after the timed region.
+    instrumented_steps = 3
+    plane.timer = in_step = KernelTimer()
+    for _ in range(instrumented_steps):
+        step()
+    drain()
+    plane.timer = None
+    kernels = dict(in_step.summary(), gather=timer.summary()["gather"])
+    launches = kernels["restore"]["launches"] // instrumented_steps
 
     # Parity of the last step, outside the timed region.
     import oracle
@@ -298,7 +307,7 @@ def run_save_restore(args):
 
     gather, restore, crc, sha = kernels["gather"], kernels["restore"], kernels["crc32c"], kernels["sha256"]
     gather_achieved = 2 * total / (gather["avg_ms"] * 1e6)          # read + write, one launch per save
-    restore_link = (total * args.steps / restore["launches"]) / (restore["avg_ms"] * 1e6)
+    restore_link = (total * instrumented_steps / restore["launches"]) / (restore["avg_ms"] * 1e6)
     # After the timed region, on the session's records gathered into device memory: the scatter (the
     # verified restore's last step) into the restore targets, which already hold the same bytes, and the
     # CRC32C kernel alone (in the steps it shares the GPU with earlier saves' SHA-256 kernels).
@@ -365,6 +374,8 @@ def run_save_restore(args):
         "restore_frac_of_pcie5_x16": round(total / lat["restore"] / 1e6 / PCIE5_X16_GBPS, 4),
         "save_frac_of_pcie5_x16": round(total / lat["save"] / 1e6 / PCIE5_X16_GBPS, 4),
         "kernels_ms": {name: round(k["avg_ms"], 4) for name, k in kernels.items()},
+        "kernels_ms_source": "gather: HIP events in the timed steps; the others: 3 steps after them with every "
+                             "launch timed",
         "roofline": {"kernel": "gather_kernel", "bound": "hbm", "achieved": round(gather_achieved, 1),
                      "peak": HBM_PEAK_GBPS, "unit": "GB/s", "frac": round(gather_achieved / HBM_PEAK_GBPS, 4),
                      "traffic": measured_traffic("gather_kernel"), "algorithmic_bytes": 2 * total,
@@ -1142,7 +1153,9 @@ def turn_cpu_baseline(tier, snapshot, size):
 def main():
     parser = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     parser.add_argument("--gpus", type=int, default=1)
-    parser.add_argument("--steps", type=int, default=10)
+    # 40 steps: the timed region ends when the last save's SHA-256 is done, about 14 ms after its restore,
+    # a tail that 10 steps would spread as 1.4 ms over each.
+    parser.add_argument("--steps", type=int, default=40)
     parser.add_argument("--warmup", type=int, default=3)
     parser.add_argument("--layout", choices=("kv_split", "vllm"), default="kv_split")
     parser.add_argument("--workload", choices=("save-restore", "disk-fork", "rotating-fp8", "turns", "cpu-roundtrip",
