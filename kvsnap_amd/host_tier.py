@@ -216,15 +216,23 @@ class HostTier:
         held until the copies have completed.  ``verify=True`` checks each
         block's CRC32C on the GPU before it reaches the cache
         (``load_scatter_verified``), where the reference checks in place on
-        the host (``volatile.py:302-305``).  The returned view has no
+        the host (``volatile.py:302-305``); ``verify="checked"`` checks it in
+        the restore's own pass (``load_scatter_checked``: no extra pass, but
+        on a mismatch the blocks hold the copied bytes and must be treated as
+        not restored).  The returned view has no
         references of its own; pass it as ``previous`` to the session's next
         save.
         """
         segments = snapshot["segments"]
         if len(block_ids) != len(segments):
             raise ValueError("one target block per segment is required")
+        if verify not in (False, True, "checked"):
+            raise ValueError("verify must be False, True or 'checked'")
         with self.borrow(segments, snapshot["locations"]) as sources:
-            if verify:
+            if verify == "checked":
+                self.plane.load_scatter_checked(list(block_ids), sources, [s["crc32c"] for s in segments],
+                                                progress=progress, chunk_bytes=chunk_bytes)
+            elif verify:
                 self.plane.load_scatter_verified(list(block_ids), sources, [s["crc32c"] for s in segments],
                                                  progress=progress, chunk_bytes=chunk_bytes)
             else:

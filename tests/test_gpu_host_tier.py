@@ -89,7 +89,7 @@ def test_delta_save_equals_a_full_save_and_gathers_only_changed_blocks(plane, or
         assert tier.stats() == dict(resident_bytes=0, blob_count=0, capacity_bytes=256 << 20)
 
 
-@pytest.mark.parametrize("verify", [False, True])
+@pytest.mark.parametrize("verify", [False, True, "checked"])
 def test_restore_from_the_tier_then_delta_save_into_the_restored_blocks(plane, oracle_lib, verify):
     rng = random.Random(3)
     ids = rng.sample(range(1, BLOCKS), 40)
@@ -146,6 +146,27 @@ def test_a_corrupted_held_block_is_refused_by_the_verified_restore(plane):
     assert torch.equal(plane.backing.view(torch.int16), before), "no KV block is written"
     byte.value ^= 0x10
     tier.restore(ids[4:], snapshot, verify=True)
+    tier.release(snapshot)
+
+
+def test_a_corrupted_held_block_fails_the_checked_restore_after_its_copy(plane):
+    ids = random.Random(7).sample(range(1, BLOCKS), 8)
+    tier = HostTier(plane, 256 << 20)
+    snapshot = tier.save(ids[:4], 4 * BLOCK_SIZE)
+    held = tier._entries[snapshot["segments"][1]["blob_id"]]["allocation"]
+    byte = C.c_uint8.from_address(held.pointer + 54321)
+    byte.value ^= 0x01
+    progress = []
+    with pytest.raises(CorruptSnapshotError, match=r"1 of 4 .*block 1\)"):
+        tier.restore(ids[4:], snapshot, verify="checked", progress=progress)
+    assert progress == []
+    byte.value ^= 0x01
+    tier.restore(ids[4:], snapshot, verify="checked")
+    torch.cuda.synchronize()
+    src, dst = torch.tensor(ids[:4], device="cuda"), torch.tensor(ids[4:], device="cuda")
+    assert torch.equal(plane.backing[:, :, dst].view(torch.int16), plane.backing[:, :, src].view(torch.int16))
+    with pytest.raises(ValueError):
+        tier.restore(ids[4:], snapshot, verify="staged")
     tier.release(snapshot)
 
 
