@@ -220,26 +220,31 @@ def run_save_restore(args):
     log(f"DMA peaks: H2D {h2d_peak:.1f} GB/s, D2H {d2h_peak:.1f} GB/s")
 
     # Latency, one operation at a time (not the timed region): save until the
-    # D2H fence, save until its CRC32C and SHA-256 are ready, restore, the
-    # restore's early-readiness point, and the checked restore (every block's
-    # CRC32C folded in as it is copied, then compared with the save's).
-    # Medians of five (all five reported): in
-    # the second and later processes on a box, one restore launch of the third
-    # sample has stalled for 17-44 ms.
+    # D2H fence, save until its CRC32C and SHA-256 are ready, restore, and the
+    # checked restore (every block's CRC32C folded in as it is copied, then
+    # compared with the save's), none of them carrying timing events (events
+    # around each of a restore's 19 launches add 0.24 ms to it).  Then a
+    # restore and a checked restore with every launch timed, for the
+    # early-readiness point and the per-launch kernel times.  Medians of five
+    # (all five reported): in the second and later processes on a box, one
+    # restore launch of the third sample has stalled for 17-44 ms.
     latency = {"save": [], "hashed": [], "restore": [], "early": [], "checked": []}
     lat_timer = KernelTimer()
     for i in range(6):
-        plane.timer = lat_timer if i else None
         digests, progress = [], []
         t0 = time.perf_counter()
         plane.save_gather(source, targets, tokens, digests=digests)
         t1 = time.perf_counter()
         saved_crcs = [crc for _, crc in digests[0].result()]
         t2 = time.perf_counter()
-        plane.load_scatter(target, targets, progress=progress)
+        plane.load_scatter(target, targets)
         t3 = time.perf_counter()
         plane.load_scatter_checked(target, targets, saved_crcs)
         t4 = time.perf_counter()
+        plane.timer = lat_timer if i else None
+        plane.load_scatter(target, targets, progress=progress)
+        plane.load_scatter_checked(target, targets, saved_crcs)
+        plane.timer = None
         if i:
             latency["checked"].append((t4 - t3) * 1e3)
             latency["save"].append((t1 - t0) * 1e3)
@@ -248,7 +253,6 @@ def run_save_restore(args):
             launches = len(progress) - 1
             pairs = lat_timer.pairs["restore"][-launches:]
             latency["early"].append(pairs[0][0].elapsed_time(pairs[early_launch_index(progress)][1]))
-    plane.timer = None
     lat = {k: statistics.median(v) for k, v in latency.items()}
     checked_launch_ms = lat_timer.summary()["restore_checked"]["avg_ms"]
 
