@@ -89,10 +89,12 @@ def test_a_saved_snapshot_restores_bit_for_bit_into_shuffled_blocks(planes, rest
             allocation.close()
 
 
-def test_saves_and_restores_from_two_threads_overlap_byte_exact(planes):
+@pytest.mark.parametrize("checked", [False, True])
+def test_saves_and_restores_from_two_threads_overlap_byte_exact(planes, checked):
     """The connector's save thread and loader thread at once (reference vllm.py:202-203), restores on their
     own stream through the copy engines: session k is restored while session k + 1 is saved into the other
-    pinned buffer.  Every restore must hold exactly the bytes its save saw."""
+    pinned buffer.  Every restore must hold exactly the bytes its save saw; checked restores also pass the
+    CRC32Cs their save computed on the GPU."""
     import threading
     caches, backing = synth.make_caches(LAYERS, 96, layout="kv_split")
     plane = planes(caches, capacity=2 * 16 * LAYERS * 65536 + (64 << 20), restore_stream="split",
@@ -132,7 +134,11 @@ def test_saves_and_restores_from_two_threads_overlap_byte_exact(planes):
                 saved[k].wait(60)
                 if failures:
                     return
-                plane.load_scatter(target, targets[k % 2], chunk_bytes=5 * size)
+                if checked:
+                    crcs = [crc for _, crc in digests[k].result()]
+                    plane.load_scatter_checked(target, targets[k % 2], crcs, chunk_bytes=5 * size)
+                else:
+                    plane.load_scatter(target, targets[k % 2], chunk_bytes=5 * size)
                 torch.cuda.synchronize()
                 if not torch.equal(backing[:, :, dst].view(torch.int16), expected[k].view(torch.int16)):
                     failures.append(AssertionError(f"restore {k} differs from save {k}"))
