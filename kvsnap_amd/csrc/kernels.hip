@@ -30,6 +30,7 @@
 
 #include "common.h"
 
+#include <algorithm>
 #include <cstdint>
 #include <cstring>
 #include <mutex>
@@ -353,58 +354,60 @@ __global__ __launch_bounds__(kThreads) void synth_decode_kernel(const int64_t* _
 //   satisfies R(A || B) = shift(R(A), |B|) ^ R(B) and R(0^k || A) = R(A).
 // So a record can be cut into equal stripes (the first one padded in front
 // with virtual zero bytes) whose raw CRCs are computed independently and
-// combined by Horner's rule; crc32c = ~(shift(~prior, N) ^ R(record)).
+// combined; crc32c = ~(shift(~prior, N) ^ R(record)).
 //
-// Inside a stripe, lane t of a 1024-lane workgroup reads the 16-byte word at
-// t*16 of every 16 KiB group (fully coalesced; a batch of 8 groups is loaded
-// before any is folded, so a lane has 8 loads in flight), folds them with
-//   acc = shift(acc, 16384) ^ R16(word),
-// and finally contributes shift(acc, (1023 - t) * 16); the workgroup's XOR of
-// those is the stripe's raw CRC.  R16 runs slicing-by-4 over the word's four
-// dwords, s = S0[b0] ^ S1[b1] ^ S2[b2] ^ S3[b3] of (s ^ dword), with
-//   S[i][v]  = shift(v, 4 - i)
-// and the per-group advance uses
-//   G[k][v]  = shift(v << 8k, 16384).
-// Per-lane constants M[t] = x^(8 * 16 * (1023 - t)) mod P are applied with a
-// bitwise GF(2) multiply.
+// A stripe is one wave's job: `groups` groups of 4 KiB, lane l folding the 64
+// contiguous bytes at l * 64 of every group (four 16-byte loads; the four
+// loads of a wave together cover the group's lines).  A lane's bytes of one
+// group are one slicing-by-4 chain of 16 dwords, with no step between them,
+// and the lane moves to the next group of its chain with one "advance" of 4
+// lookups.  Two chains per lane (even and odd groups of the stripe) keep two
+// independent lookup streams in flight; a chain's runs are 8 KiB apart, so
+//   acc' = chain(advance(acc), run),   advance(s) = shift(s, 8192 - 64),
+// and the chain itself shifts by the run's 64 bytes.  At the end the odd
+// chain's register is shifted past the group it lacks, each lane's register
+// past the lanes after it (per-lane constants), and the wave's XOR is the
+// stripe's raw CRC.  A combine kernel shifts every stripe to its record's end
+// (one wave per record) and adds the initial value's term.
 //
-// The lookups are the kernel's cost, and random 8-bit indices into one shared
-// 1 KiB table put several lanes of a wave on the same LDS bank (61 % of the
-// LDS cycles were bank conflicts with shared tables).  So every lane reads
-// its own copy of S: entry v of S[i] for lane t sits at byte
+//   S[i][v] = shift(v, 4 - i)                (slicing-by-4, one dword)
+//   G[k][v] = shift(v << 8k, 8192 - 64)      (a chain's advance)
+//   H[k][v] = shift(v << 8k, 4096)           (the chain behind, one group on)
+//   M[l]    = x^(8 * 64 * (63 - l)) mod P    (lane l's run to the group's end)
+//
+// The lookups are the kernel's cost.  Random 8-bit indices into one shared
+// 1 KiB table put several lanes of a wave on one LDS bank, so every lane
+// reads its own copy of S: entry v of S[i] for lane t sits at byte
 //   4096 + (i / 2) * 65536 + v * 256 + (i % 2) * 128 + (t % 32) * 4,
-// i.e. in bank t % 32, and the 32 lanes that an LDS pass serves never share a
-// bank.  The address is one byte move (v into byte 1 of a per-lane constant;
-// the 4096 rides in the instruction's offset field).  The four copies fill
-// 128 KiB of the 160 KiB LDS, so a CU holds one workgroup; the 4 KiB of G
-// stay shared (4 of the 20 lookups per word) at the front of the LDS, where
-// each table's base also fits the offset field.
-// A stripe is 8-48 groups (128-768 KiB), chosen per record size and count
-// (crc_plan); groups that hold only front padding are skipped.  One batch in
-// flight per lane measured as fast as two (software-pipelined), and 8-group
-// batches beat 16 (5.6-5.9 against 5.2-5.6 TB/s): a 1024-lane workgroup with
-// 256 KiB of loads in flight is past what the memory system serves best, as
-// a plain read kernel of the same shape also shows.
-
+// in bank t % 32, and the 32 lanes an LDS pass serves never share a bank.
+// The address is one byte move (v into byte 1 of a per-lane constant; the
+// 4096 rides in the instruction's offset field).  The copies fill 128 KiB of
+// the LDS, so a CU holds one 1024-lane workgroup.  G (4 KiB) stays shared at
+// the front of the LDS; with 64-byte runs it takes 4 of every 68 lookups
+// (with one 16-byte word per lane and group it was 4 of 20, and its bank
+// conflicts were 29 % of the LDS's active cycles).
 constexpr uint32_t kPoly = 0x82F63B78u;
 constexpr int kCrcThreads = 1024;
-constexpr int kCrcGroup = kCrcThreads * 16;  // bytes per group: one 16-byte word per lane
-constexpr int kCrcBatch = 8;                // groups loaded before they are folded
-constexpr int kCrcMaxGroups = (768 << 10) / kCrcGroup;  // stripes of at most 768 KiB
-constexpr int kCrcResident = 256;            // workgroups resident at once: one per CU
-// Launch grid cap: twice the resident count.  Beside a save's SHA-256 kernels
-// (whose workgroups hold a CU's LDS) a one-per-CU persistent grid waits for
-// its last workgroups to find a CU (0.283 ms in the pipelined step against
-// 0.250 at 512 and 0.241 with one workgroup per job, which costs 8 % alone).
-constexpr int kCrcGrid = 512;
+constexpr int kCrcWaves = kCrcThreads / 64;
+constexpr int kCrcRun = 16;                  // bytes one lane folds per group: one 16-byte word
+constexpr int kCrcChains = 8;                // groups per batch, each its own chain
+constexpr bool kCrcNontemporal = true;       // streaming loads
+constexpr int kCrcRunWords = kCrcRun / 16;
+constexpr int kCrcBatchWords = kCrcChains * kCrcRunWords;  // 16-byte loads per lane per batch
+constexpr int kCrcGroup = 64 * kCrcRun;      // one wave's group
+constexpr int kCrcMaxStripes = 64;           // per record: the combine's lanes
+constexpr int kCrcResidentWaves = 256 * kCrcWaves;  // one workgroup per CU
 constexpr int kCrcAdvanceBytes = 4 * 1024;   // G, shared, at LDS byte 0
 constexpr int kCrcPrivateBytes = 2 * 65536;  // the lanes' copies of S, after G
+constexpr int kCrcBehindBytes = 4 * 1024;    // H, shared, after S
 
-// g_crc_tables: S[4][256], then G[4][256], then M[kCrcThreads].
+// g_crc_tables: S[4][256], then G[4][256], then H[4][256], then M[64].
 constexpr int kCrcAdvance = 4 * 256;
-constexpr int kCrcLaneShift = kCrcAdvance + 4 * 256;
+constexpr int kCrcBehind = kCrcAdvance + 4 * 256;
+constexpr int kCrcLaneShift = kCrcBehind + 4 * 256;
+constexpr int kCrcTableWords = kCrcLaneShift + 64;
 
-__device__ uint32_t g_crc_tables[kCrcLaneShift + kCrcThreads];
+__device__ uint32_t g_crc_tables[kCrcTableWords];
 
 __device__ __forceinline__ uint32_t gf_mul(uint32_t a, uint32_t b) {
     // a * b mod P in the reflected representation (bit 31 is x^0).
@@ -432,7 +435,65 @@ __device__ __forceinline__ uint32_t crc_columns(uint32_t lane) {
     return col | ((col + 128u) << 8) | (1u << 16);
 }
 
-// One dword through slicing-by-4 from x = state ^ dword.  v_perm_b32 picks
+// shift(acc, d) for the distance d its table G (at LDS byte 0) was built for.
+__device__ __forceinline__ uint32_t crc_advance(const uint32_t* lds, uint32_t acc) {
+    return xor3(lds_word(lds, (acc & 0xFFu) << 2), lds_word(lds, 1024u + (((acc >> 8) & 0xFFu) << 2)),
+                lds_word(lds, 2048u + (((acc >> 16) & 0xFFu) << 2))) ^
+           lds_word(lds, 3072u + ((acc >> 24) << 2));
+}
+
+// The run of lane `lane` in the group at record offset `group_at` (which may
+// lie partly or wholly in the front padding: those bytes are zero).
+template <bool kAligned>
+__device__ __forceinline__ void crc_load_run(const uint8_t* __restrict__ rec, int64_t group_at, uint32_t lane,
+                                             u32x4* v) {
+    const int64_t at = group_at + static_cast<int64_t>(lane) * kCrcRun;
+#pragma unroll
+    for (int k = 0; k < kCrcRunWords; ++k) {
+        v[k] = u32x4{0u, 0u, 0u, 0u};
+        const int64_t word = at + 16 * k;
+        if (kAligned) {
+            // The padding is a multiple of 16 here, so a word is all padding or all record.
+            if (word >= 0) v[k] = *reinterpret_cast<const u32x4*>(rec + word);
+        } else {
+            uint32_t w[4] = {0, 0, 0, 0};
+            for (int b = 0; b < 16; ++b)
+                if (word + b >= 0) w[b >> 2] |= static_cast<uint32_t>(rec[word + b]) << (8 * (b & 3));
+            v[k] = u32x4{w[0], w[1], w[2], w[3]};
+        }
+    }
+}
+
+// A batch of whole groups of record bytes at record offset `at` (>= 0, 16-byte aligned): chain c's run at
+// v[c * kCrcRunWords ...].
+__device__ __forceinline__ void crc_load_batch(const uint8_t* __restrict__ rec, int64_t at, uint32_t lane, u32x4* v) {
+    const u32x4* p = reinterpret_cast<const u32x4*>(rec + at + static_cast<int64_t>(lane) * kCrcRun);
+#pragma unroll
+    for (int c = 0; c < kCrcChains; ++c)
+#pragma unroll
+        for (int k = 0; k < kCrcRunWords; ++k) {
+            const u32x4* q = p + c * (kCrcGroup / 16) + k;
+            v[c * kCrcRunWords + k] = kCrcNontemporal ? __builtin_nontemporal_load(q) : *q;
+        }
+}
+
+// Any batch: the first may hold front padding, the last may hold fewer than kCrcChains groups.
+template <bool kAligned>
+__device__ __forceinline__ void crc_load_any(const uint8_t* __restrict__ rec, int64_t at, int count, uint32_t lane,
+                                             u32x4* v) {
+#pragma unroll
+    for (int c = 0; c < kCrcChains; ++c) {
+        if (c < count) {
+            crc_load_run<kAligned>(rec, at + static_cast<int64_t>(c) * kCrcGroup, lane, v + c * kCrcRunWords);
+        } else {
+#pragma unroll
+            for (int k = 0; k < kCrcRunWords; ++k) v[c * kCrcRunWords + k] = u32x4{0u, 0u, 0u, 0u};
+        }
+    }
+}
+
+// One dword through slicing-by-4 looks up the four bytes of x = state ^
+// dword.  v_perm_b32 picks
 // bytes of {S0 = x (bytes 4-7), S1 = cols (bytes 0-3)}, selector 12 giving
 // 0x00: the address of S[i][byte i of x] is byte i of x in byte 1 above the
 // lane's column, one instruction per lookup:
@@ -440,118 +501,268 @@ __device__ __forceinline__ uint32_t crc_columns(uint32_t lane) {
 //   S[1]: (x & 0xFF00) | (col + 128)                  selector 0x0C0C0501
 //   S[2]: 0x10000 | ((x >> 8) & 0xFF00) | col          selector 0x0C020600
 //   S[3]: 0x10000 | ((x >> 16) & 0xFF00) | (col + 128) selector 0x0C020701
-__device__ __forceinline__ uint32_t crc_dword(const uint32_t* lds, uint32_t cols, uint32_t x) {
-    const uint32_t* s = lds + kCrcAdvanceBytes / 4;
-    const uint32_t a = lds_word(s, __builtin_amdgcn_perm(x, cols, 0x0C0C0400u));
-    const uint32_t b = lds_word(s, __builtin_amdgcn_perm(x, cols, 0x0C0C0501u));
-    const uint32_t c = lds_word(s, __builtin_amdgcn_perm(x, cols, 0x0C020600u));
-    const uint32_t d = lds_word(s, __builtin_amdgcn_perm(x, cols, 0x0C020701u));
-    return xor3(a, b, c) ^ d;
+// One slicing-by-4 step of every chain at once: all the chains' lookups are
+// issued before any result is used, so a wave keeps 4 * kCrcChains LDS reads
+// in flight (left to itself the compiler runs the chains one after another,
+// each step waiting out a whole LDS round trip).
+__device__ __forceinline__ void crc_step_all(const uint32_t* lds, uint32_t cols, uint32_t* s, const uint32_t* data) {
+    const uint32_t* tab = lds + kCrcAdvanceBytes / 4;
+    uint32_t r[kCrcChains][4];
+#pragma unroll
+    for (int c = 0; c < kCrcChains; ++c) {
+        const uint32_t x = s[c] ^ data[c];
+        r[c][0] = lds_word(tab, __builtin_amdgcn_perm(x, cols, 0x0C0C0400u));
+        r[c][1] = lds_word(tab, __builtin_amdgcn_perm(x, cols, 0x0C0C0501u));
+        r[c][2] = lds_word(tab, __builtin_amdgcn_perm(x, cols, 0x0C020600u));
+        r[c][3] = lds_word(tab, __builtin_amdgcn_perm(x, cols, 0x0C020701u));
+    }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int c = 0; c < kCrcChains; ++c) s[c] = xor3(r[c][0], r[c][1], r[c][2]) ^ r[c][3];
+    __builtin_amdgcn_sched_barrier(0);
 }
 
-__device__ __forceinline__ uint32_t crc_word(const uint32_t* lds, uint32_t cols, u32x4 v) {
-    uint32_t s = crc_dword(lds, cols, v.x);
-    s = crc_dword(lds, cols, s ^ v.y);
-    s = crc_dword(lds, cols, s ^ v.z);
-    return crc_dword(lds, cols, s ^ v.w);
+// Fold a batch: chain c advances to its next run and takes it through slicing-by-4.  Chains past `count`
+// (the last batch's missing groups) are left alone.
+__device__ __forceinline__ void crc_fold_batch(const uint32_t* lds, uint32_t cols, const u32x4* v, uint32_t* acc,
+                                               int count) {
+    uint32_t s[kCrcChains], r[kCrcChains][4];
+#pragma unroll
+    for (int c = 0; c < kCrcChains; ++c) {
+        r[c][0] = lds_word(lds, (acc[c] & 0xFFu) << 2);
+        r[c][1] = lds_word(lds, 1024u + (((acc[c] >> 8) & 0xFFu) << 2));
+        r[c][2] = lds_word(lds, 2048u + (((acc[c] >> 16) & 0xFFu) << 2));
+        r[c][3] = lds_word(lds, 3072u + ((acc[c] >> 24) << 2));
+    }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int c = 0; c < kCrcChains; ++c) s[c] = xor3(r[c][0], r[c][1], r[c][2]) ^ r[c][3];
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int k = 0; k < kCrcRunWords; ++k) {
+        uint32_t d[kCrcChains];
+#pragma unroll
+        for (int c = 0; c < kCrcChains; ++c) d[c] = v[c * kCrcRunWords + k].x;
+        crc_step_all(lds, cols, s, d);
+#pragma unroll
+        for (int c = 0; c < kCrcChains; ++c) d[c] = v[c * kCrcRunWords + k].y;
+        crc_step_all(lds, cols, s, d);
+#pragma unroll
+        for (int c = 0; c < kCrcChains; ++c) d[c] = v[c * kCrcRunWords + k].z;
+        crc_step_all(lds, cols, s, d);
+#pragma unroll
+        for (int c = 0; c < kCrcChains; ++c) d[c] = v[c * kCrcRunWords + k].w;
+        crc_step_all(lds, cols, s, d);
+    }
+#pragma unroll
+    for (int c = 0; c < kCrcChains; ++c)
+        if (c < count) acc[c] = s[c];
 }
 
-__device__ __forceinline__ uint32_t crc_advance(const uint32_t* lds, uint32_t acc) {
-    return xor3(lds_word(lds, (acc & 0xFFu) << 2), lds_word(lds, 1024u + (((acc >> 8) & 0xFFu) << 2)),
-                lds_word(lds, 2048u + (((acc >> 16) & 0xFFu) << 2))) ^
-           lds_word(lds, 3072u + ((acc >> 24) << 2));
+// The batches of one stripe after its first (already in `cur`, `count` groups, folded next), with the
+// batch after the current one loaded while the current one is folded (two register buffers).  In the
+// steady state every prefetch is a whole batch of record bytes and unconditional, so the wait for the
+// current batch lets the prefetch's loads stay in flight.  The last batch may hold fewer groups than
+// chains; it is loaded once the one before it is folded.
+template <bool kAligned>
+__device__ __forceinline__ void crc_fold_rest(const uint32_t* lds, uint32_t cols, const uint8_t* __restrict__ rec,
+                                              int64_t start, int groups, int g, int count, uint32_t lane, u32x4* cur,
+                                              uint32_t* acc) {
+    crc_fold_batch(lds, cols, cur, acc, count);
+    g += kCrcChains;
+    if (g < groups) {
+        const int left = groups - g;
+        crc_load_any<kAligned>(rec, start + static_cast<int64_t>(g) * kCrcGroup, left, lane, cur);
+        crc_fold_batch(lds, cols, cur, acc, left);
+    }
 }
 
+// The LDS tables of a CRC workgroup: G shared at byte 0, the lanes' private
+// copies of S, then H shared.
+__device__ __forceinline__ void crc_fill_tables(uint32_t* lds) {
+    // Thread t owns S entry t (table t / 256, value t % 256): one read, then its 32 lane columns are one
+    // 128-byte run of the private layout, written as eight 16-byte stores.
+    static_assert(kCrcThreads == 4 * 256, "one thread per table entry");
+    const uint32_t t = threadIdx.x, table = t >> 8, v = t & 255u;
+    const uint32_t word = g_crc_tables[t];
+    const u32x4 four = {word, word, word, word};
+    u32x4* run = reinterpret_cast<u32x4*>(reinterpret_cast<char*>(lds) + kCrcAdvanceBytes + (table >> 1) * 65536u +
+                                          v * 256u + (table & 1u) * 128u);
+#pragma unroll
+    for (int k = 0; k < 8; ++k) run[k] = four;
+    lds[t] = g_crc_tables[kCrcAdvance + t];
+    lds[(kCrcAdvanceBytes + kCrcPrivateBytes) / 4 + t] = g_crc_tables[kCrcBehind + t];
+}
+
+// One wave's job: the raw CRC of the stripe of `groups` groups whose first byte is at record offset
+// `start` (negative in the first stripe: front padding), the XOR of the wave's lanes.
+template <bool kAligned>
+__device__ __forceinline__ uint32_t crc_stripe(const uint32_t* lds, uint32_t lane, uint32_t cols, uint32_t lane_shift,
+                                               const uint8_t* __restrict__ rec, int64_t start, int groups) {
+    const uint32_t* behind_table = lds + (kCrcAdvanceBytes + kCrcPrivateBytes) / 4;
+    // Groups of padding only (in stripe 0) are skipped, not folded: the registers are still zero there.
+    const int lead = start < 0 ? static_cast<int>((-start) / kCrcGroup) : 0;
+    // Chain c takes groups lead + c, lead + c + kCrcChains, ...  Only the first batch may hold front
+    // padding, and only the last may hold fewer groups than chains.
+    uint32_t acc[kCrcChains];
+#pragma unroll
+    for (int c = 0; c < kCrcChains; ++c) acc[c] = 0;
+    u32x4 a[kCrcBatchWords], b[kCrcBatchWords];
+    int g = lead;
+    const int count = groups - g < kCrcChains ? groups - g : kCrcChains;
+    {
+        const int64_t at = start + static_cast<int64_t>(g) * kCrcGroup;
+        if (kAligned && at >= 0 && count == kCrcChains)
+            crc_load_batch(rec, at, lane, a);
+        else
+            crc_load_any<kAligned>(rec, at, count, lane, a);
+    }
+    // The first batch's loads are complete before the steady state starts, which the wait for its
+    // prefetches then counts on (vmcnt(0); expcnt and lgkmcnt left alone).
+    __builtin_amdgcn_s_waitcnt(0x0F70);
+    while (true) {
+        if (g + 2 * kCrcChains > groups) {
+            crc_fold_rest<kAligned>(lds, cols, rec, start, groups, g, count, lane, a, acc);
+            break;
+        }
+        crc_load_batch(rec, start + static_cast<int64_t>(g + kCrcChains) * kCrcGroup, lane, b);
+        crc_fold_batch(lds, cols, a, acc, kCrcChains);
+        g += kCrcChains;
+        if (g + 2 * kCrcChains > groups) {
+            crc_fold_rest<kAligned>(lds, cols, rec, start, groups, g, kCrcChains, lane, b, acc);
+            break;
+        }
+        crc_load_batch(rec, start + static_cast<int64_t>(g + kCrcChains) * kCrcGroup, lane, a);
+        crc_fold_batch(lds, cols, b, acc, kCrcChains);
+        g += kCrcChains;
+    }
+    // Horner over the chains in the order of their last groups: the chain whose last group is d groups
+    // before the stripe's end is (m - 1 - d) mod kCrcChains, m the groups folded; chains that took no
+    // group hold zero.
+    const int m = groups - lead;
+    uint32_t x = 0;
+#pragma unroll
+    for (int d = kCrcChains - 1; d >= 0; --d) {
+        const int c = ((m - 1 - d) % kCrcChains + kCrcChains) % kCrcChains;  // wave-uniform
+        uint32_t pick = acc[0];
+#pragma unroll
+        for (int k = 1; k < kCrcChains; ++k) pick = c == k ? acc[k] : pick;
+        x = (d == kCrcChains - 1 ? 0u : crc_advance(behind_table, x)) ^ pick;
+    }
+    // The lane's constant is the same for every job: hidden from the compiler here, or it keeps the
+    // multiply's 32 masks live across the job loop.
+    uint32_t shift = lane_shift;
+    asm volatile("" : "+v"(shift));
+    x = gf_mul(shift, x);
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) x ^= __shfl_xor(x, o);
+    return x;
+}
+
+// x^(8 * stripe_bytes * 2^i) mod P: the shifts of a stripe past the ones after it.
+struct CrcStripePowers {
+    uint32_t p[6];
+};
+
+__device__ __forceinline__ uint32_t crc_shift_stripes(const CrcStripePowers& powers, int behind, uint32_t x) {
+#pragma unroll
+    for (int i = 0; i < 6; ++i)
+        if ((behind >> i) & 1) x = gf_mul(powers.p[i], x);
+    return x;
+}
+
+// Jobs spread over the chip: the waves take (record, stripe) jobs in turn and
+// write each stripe's raw CRC to `partial`; crc_combine_kernel then gives the
+// records' CRC32C.  For few records, whose stripes must spread over many CUs.
 template <bool kAligned>
 __global__ __launch_bounds__(kCrcThreads) void crc_stripes_kernel(const uint8_t* __restrict__ records, uint64_t pitch,
                                                                  int64_t n_records, int64_t stripes, int groups,
                                                                  uint64_t pad, uint32_t* __restrict__ partial) {
-    __shared__ uint32_t lds[(kCrcAdvanceBytes + kCrcPrivateBytes) / 4];
-    __shared__ uint32_t red[kCrcThreads / 64];
-    for (int i = threadIdx.x; i < kCrcAdvanceBytes / 4; i += kCrcThreads) lds[i] = g_crc_tables[kCrcAdvance + i];
-    for (int w = threadIdx.x; w < kCrcPrivateBytes / 4; w += kCrcThreads) {
-        // word w of S: 64 KiB half w >> 14, entry (w >> 6) & 255, column w & 63 (table 2 * half + column / 32)
-        const int table = ((w >> 14) << 1) | ((w >> 5) & 1);
-        lds[kCrcAdvanceBytes / 4 + w] = g_crc_tables[table * 256 + ((w >> 6) & 255)];
-    }
-    const uint32_t lane_shift = g_crc_tables[kCrcLaneShift + threadIdx.x];
-    const uint32_t cols = crc_columns(threadIdx.x);
+    __shared__ uint32_t lds[(kCrcAdvanceBytes + kCrcPrivateBytes + kCrcBehindBytes) / 4];
+    crc_fill_tables(lds);
+    const uint32_t lane = threadIdx.x & 63u;
+    const uint32_t lane_shift = g_crc_tables[kCrcLaneShift + lane];
+    const uint32_t cols = crc_columns(lane);
     __syncthreads();
-    const int64_t jobs = n_records * stripes;
+    // Jobs, records and stripes fit 32 bits (the host checks): 32-bit job arithmetic keeps the scalar
+    // registers free of 64-bit division.
+    const uint32_t jobs = static_cast<uint32_t>(n_records) * static_cast<uint32_t>(stripes);
+    const uint32_t waves = gridDim.x * kCrcWaves;
     const int64_t stripe_bytes = static_cast<int64_t>(groups) * kCrcGroup;
-    for (int64_t job = blockIdx.x; job < jobs; job += gridDim.x) {
-        const int64_t r = job / stripes, j = job - r * stripes;
-        const uint8_t* rec = records + r * pitch;
-        uint32_t acc = 0;
-        for (int g0 = 0; g0 < groups; g0 += kCrcBatch) {
-            const int n = groups - g0 < kCrcBatch ? groups - g0 : kCrcBatch;  // workgroup-uniform
-            const int64_t batch_at = j * stripe_bytes + static_cast<int64_t>(g0) * kCrcGroup - static_cast<int64_t>(pad);
-            if (kAligned && n == kCrcBatch && batch_at >= 0) {
-                // A whole batch of record groups: no padding, no predicates.  The words' slicing chains
-                // are independent, so they interleave; the advance chain follows.
-                const u32x4* at = reinterpret_cast<const u32x4*>(rec + batch_at) + threadIdx.x;
-                u32x4 v[kCrcBatch];
+    const uint32_t first = blockIdx.x * kCrcWaves + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    for (uint32_t job = first; job < jobs; job += waves) {
+        const uint32_t r = job / static_cast<uint32_t>(stripes), j = job - r * static_cast<uint32_t>(stripes);
+        const int64_t start = static_cast<int64_t>(j) * stripe_bytes - static_cast<int64_t>(pad);
+        const uint32_t x = crc_stripe<kAligned>(lds, lane, cols, lane_shift, records + static_cast<int64_t>(r) * pitch,
+                                                start, groups);
+        if (lane == 0) partial[job] = x;
+    }
+}
+
+// Whole records per workgroup: a round gives `per_group` records' stripes to
+// the workgroup's waves (wave w: record w / stripes, stripe w % stripes),
+// each wave shifts its stripe's raw CRC to the record's end, and the
+// workgroup XORs them in LDS, so no second launch combines them.  For many
+// records (the chip fills with a few stripes each).
+template <bool kAligned>
+__global__ __launch_bounds__(kCrcThreads) void crc_records_kernel(const uint8_t* __restrict__ records, uint64_t pitch,
+                                                                 int64_t n_records, int stripes, int groups,
+                                                                 uint64_t pad, CrcStripePowers powers,
+                                                                 uint32_t init_term, uint32_t* __restrict__ out) {
+    __shared__ uint32_t lds[(kCrcAdvanceBytes + kCrcPrivateBytes + kCrcBehindBytes) / 4];
+    __shared__ uint32_t stripe_crc[kCrcWaves];
+    crc_fill_tables(lds);
+    const uint32_t lane = threadIdx.x & 63u;
+    const uint32_t lane_shift = g_crc_tables[kCrcLaneShift + lane];
+    const uint32_t cols = crc_columns(lane);
+    const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
+    const int per_group = kCrcWaves / stripes;
+    const int rec_in_round = wave / stripes, j = wave - rec_in_round * stripes;
+    const int64_t stripe_bytes = static_cast<int64_t>(groups) * kCrcGroup;
+    __syncthreads();
+    for (int64_t base = static_cast<int64_t>(blockIdx.x) * per_group; base < n_records;
+         base += static_cast<int64_t>(gridDim.x) * per_group) {
+        const int64_t r = base + rec_in_round;
+        if (rec_in_round < per_group && r < n_records) {  // wave-uniform
+            // The wave's stripe is the same every round: hidden here, or what the compiler derives from it
+            // stays live across rounds and the registers spill.
+            int64_t start = static_cast<int64_t>(j) * stripe_bytes - static_cast<int64_t>(pad);
+            asm volatile("" : "+s"(start));
+            uint32_t x = crc_stripe<kAligned>(lds, lane, cols, lane_shift, records + r * pitch, start, groups);
+            const int behind = stripes - 1 - j;
 #pragma unroll
-                for (int g = 0; g < kCrcBatch; ++g) v[g] = __builtin_nontemporal_load(at + g * (kCrcGroup / 16));
-                // Keep all the batch's loads ahead of its first fold (the scheduler would otherwise wait on
-                // the first load before issuing the rest).
-                __builtin_amdgcn_sched_barrier(0);
-                uint32_t r[kCrcBatch];
-#pragma unroll
-                for (int g = 0; g < kCrcBatch; ++g) r[g] = crc_word(lds, cols, v[g]);
-#pragma unroll
-                for (int g = 0; g < kCrcBatch; ++g) acc = crc_advance(lds, acc) ^ r[g];
-                continue;
-            }
-            u32x4 v[kCrcBatch];
-#pragma unroll
-            for (int g = 0; g < kCrcBatch; ++g) {
-                v[g] = u32x4{0u, 0u, 0u, 0u};
-                // Record-relative offsets; bytes before the record (front padding) are zero.
-                const int64_t group_at = j * stripe_bytes + static_cast<int64_t>(g0 + g) * kCrcGroup -
-                                         static_cast<int64_t>(pad);  // workgroup-uniform
-                const int64_t at = group_at + threadIdx.x * 16;
-                if (g >= n || group_at + kCrcGroup <= 0) continue;  // past the stripe, or all padding
-                if (kAligned) {
-                    // The padding is a multiple of 16 here, so a word is all padding or all record.
-                    if (group_at >= 0 || at >= 0)
-                        v[g] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(rec + at));
-                } else {
-                    uint32_t w[4] = {0, 0, 0, 0};
-                    for (int k = 0; k < 16; ++k)
-                        if (at + k >= 0) w[k >> 2] |= static_cast<uint32_t>(rec[at + k]) << (8 * (k & 3));
-                    v[g] = u32x4{w[0], w[1], w[2], w[3]};
+            for (int i = 0; i < 4; ++i) {  // stripes <= 16
+                if ((behind >> i) & 1) {
+                    uint32_t power = powers.p[i];
+                    asm volatile("" : "+s"(power));  // per round, as for the lane shift
+                    x = gf_mul(power, x);
                 }
             }
-            // Groups of padding only come first, while acc is still zero: they are skipped, not folded.
-            const int64_t lead = j == 0 ? static_cast<int64_t>(pad / kCrcGroup) : 0;
-#pragma unroll
-            for (int g = 0; g < kCrcBatch; ++g)
-                if (g < n && g0 + g >= lead) acc = crc_advance(lds, acc) ^ crc_word(lds, cols, v[g]);
+            if (lane == 0) stripe_crc[wave] = x;
         }
-        uint32_t x = gf_mul(lane_shift, acc);
-#pragma unroll
-        for (int o = 32; o > 0; o >>= 1) x ^= __shfl_xor(x, o);
-        if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = x;
         __syncthreads();
-        if (threadIdx.x == 0) {
-            uint32_t sum = 0;
-#pragma unroll
-            for (int w = 0; w < kCrcThreads / 64; ++w) sum ^= red[w];
-            partial[job] = sum;
+        if (threadIdx.x < static_cast<unsigned>(per_group) && base + threadIdx.x < n_records) {
+            uint32_t x = 0;
+            for (int k = 0; k < stripes; ++k) x ^= stripe_crc[threadIdx.x * stripes + k];
+            out[base + threadIdx.x] = ~(init_term ^ x);
         }
         __syncthreads();
     }
 }
 
-__global__ __launch_bounds__(64) void crc_combine_kernel(const uint32_t* __restrict__ partial, int64_t n_records,
-                                                         int64_t stripes, uint32_t stripe_shift, uint32_t init_term,
-                                                         uint32_t* __restrict__ out) {
-    const int64_t r = static_cast<int64_t>(blockIdx.x) * 64 + threadIdx.x;
-    if (r >= n_records) return;
-    uint32_t s = 0;
-    for (int64_t j = 0; j < stripes; ++j) s = gf_mul(stripe_shift, s) ^ partial[r * stripes + j];
-    out[r] = ~(init_term ^ s);
+// One wave per record: lane j shifts stripe j's raw CRC past the stripes after it, the wave XORs them, and
+// lane 0 adds the initial value's term.
+__global__ __launch_bounds__(256) void crc_combine_kernel(const uint32_t* __restrict__ partial, int64_t n_records,
+                                                          int stripes, CrcStripePowers powers, uint32_t init_term,
+                                                          uint32_t* __restrict__ out) {
+    const int64_t r = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    if (r >= n_records) return;  // the whole wave
+    uint32_t x = 0;
+    if (lane < stripes) x = crc_shift_stripes(powers, stripes - 1 - lane, partial[r * stripes + lane]);
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) x ^= __shfl_xor(x, o);
+    if (lane == 0) out[r] = ~(init_term ^ x);
 }
 
 // ----------------------------------------------------------------- restore with CRC32C
@@ -1052,16 +1263,18 @@ void ensure_crc_tables() {
         throw std::runtime_error("no current HIP device for the CRC32C tables");
     std::lock_guard<std::mutex> lock(g_table_mutex);
     if (g_tables_ready[device]) return;
-    static uint32_t tables[kCrcLaneShift + kCrcThreads];
+    static uint32_t tables[kCrcTableWords];
     for (uint32_t i = 0; i < 4; ++i) {
         const uint32_t m = host_xpow8n(4 - i);
         for (uint32_t v = 0; v < 256; ++v) tables[256 * i + v] = host_gf_mul(m, v);
     }
-    const uint32_t group_shift = host_xpow8n(kCrcGroup);
+    const uint32_t advance = host_xpow8n(static_cast<uint64_t>(kCrcChains) * kCrcGroup - kCrcRun);
     for (uint32_t k = 0; k < 4; ++k)
-        for (uint32_t v = 0; v < 256; ++v) tables[kCrcAdvance + 256 * k + v] = host_gf_mul(group_shift, v << (8 * k));
-    for (uint32_t t = 0; t < kCrcThreads; ++t)
-        tables[kCrcLaneShift + t] = host_xpow8n(16ull * (kCrcThreads - 1 - t));
+        for (uint32_t v = 0; v < 256; ++v) tables[kCrcAdvance + 256 * k + v] = host_gf_mul(advance, v << (8 * k));
+    const uint32_t behind = host_xpow8n(kCrcGroup);
+    for (uint32_t k = 0; k < 4; ++k)
+        for (uint32_t v = 0; v < 256; ++v) tables[kCrcBehind + 256 * k + v] = host_gf_mul(behind, v << (8 * k));
+    for (uint32_t l = 0; l < 64; ++l) tables[kCrcLaneShift + l] = host_xpow8n(static_cast<uint64_t>(kCrcRun) * (63 - l));
     hipError_t rc = hipMemcpyToSymbol(HIP_SYMBOL(g_crc_tables), tables, sizeof tables, 0, hipMemcpyHostToDevice);
     if (rc != hipSuccess) throw std::runtime_error(std::string("CRC32C table upload: ") + hipGetErrorString(rc));
     // The checked restore's: G (advance by one 1 KiB row), S (slicing-by-4), M, then x^(8 * 2^k).
@@ -1129,40 +1342,93 @@ CopyShape copy_shape(int threads, int unroll, int64_t jobs, int64_t min_span_byt
 }
 
 struct CrcPlan {
-    int groups;
-    int64_t stripes;
-    uint64_t pad;
+    int groups;       // 4 KiB groups per stripe (one wave's job)
+    int64_t stripes;  // per record, at most kCrcMaxStripes
+    uint64_t pad;     // virtual zero bytes in front of each record
 };
 
-// Stripes of `groups` 16 KiB groups, the first one padded in front.  A stripe
-// is one workgroup's job and costs its real groups plus about four groups'
-// worth of per-lane multiply and reduction; whole groups of padding cost
-// nothing.  The kCrcResident resident workgroups take about
-// ceil(jobs / kCrcResident) rounds, so the plan picks the multiple of kCrcBatch up to kCrcMaxGroups
-// that minimises rounds * (groups + 4): three 768 KiB stripes per Qwen3-8B
-// record for a 512-record session, smaller stripes when few records have to
-// fill the chip.
-CrcPlan crc_plan(uint64_t record_bytes, int64_t n_records) {
+// Stripes of `groups` 4 KiB groups, the first one padded in front.  A stripe
+// is one wave's job and costs its groups plus about two groups' worth of
+// per-lane shifts and the wave's reduction; whole groups of padding cost
+// nothing.  The resident waves (16 per CU) take about
+// ceil(jobs / kCrcResidentWaves) rounds, so the plan picks the stripe count
+// (at most kCrcMaxStripes, and at most max_partials / n_records when a
+// workspace bounds it) that minimises rounds * (groups + 2): eight 288 KiB
+// stripes per Qwen3-8B record of a 512-record session (4096 jobs, one round).
+CrcPlan crc_plan(uint64_t record_bytes, int64_t n_records, int64_t max_partials = 0) {
     const uint64_t total = record_bytes ? (record_bytes + kCrcGroup - 1) / kCrcGroup : 1;
     const uint64_t n = n_records > 0 ? static_cast<uint64_t>(n_records) : 1;
-    CrcPlan plan;
-    plan.groups = static_cast<int>(total);
-    if (total > static_cast<uint64_t>(kCrcBatch)) {
-        uint64_t best = ~uint64_t(0);
-        for (int g = kCrcBatch; g <= kCrcMaxGroups; g += kCrcBatch) {
-            const uint64_t stripes = (total + g - 1) / g;
-            const uint64_t rounds = (n * stripes + kCrcResident - 1) / kCrcResident;
-            const uint64_t cost = rounds * (g + 4);
-            if (cost <= best) {
-                best = cost;
-                plan.groups = g;
-            }
+    uint64_t cap = kCrcMaxStripes;
+    if (max_partials > 0) cap = std::min<uint64_t>(cap, std::max<uint64_t>(1, static_cast<uint64_t>(max_partials) / n));
+    cap = std::min<uint64_t>(cap, total);
+    CrcPlan plan{static_cast<int>(total), 1, 0};
+    uint64_t best = ~uint64_t(0);
+    for (uint64_t s = 1; s <= cap; ++s) {
+        const uint64_t g = (total + s - 1) / s;
+        const uint64_t stripes = (total + g - 1) / g;
+        const uint64_t rounds = (n * stripes + kCrcResidentWaves - 1) / kCrcResidentWaves;
+        const uint64_t cost = rounds * (g + 2);
+        if (cost < best) {
+            best = cost;
+            plan.groups = static_cast<int>(g);
+            plan.stripes = static_cast<int64_t>(stripes);
         }
     }
-    const uint64_t stripe_bytes = static_cast<uint64_t>(plan.groups) * kCrcGroup;
-    plan.stripes = static_cast<int64_t>((total * kCrcGroup + stripe_bytes - 1) / stripe_bytes);
-    plan.pad = static_cast<uint64_t>(plan.stripes) * stripe_bytes - record_bytes;
+    plan.pad = static_cast<uint64_t>(plan.stripes) * plan.groups * kCrcGroup - record_bytes;
     return plan;
+}
+
+// Largest grid of the CRC32C launch: two workgroups per CU.  The jobs are
+// shared out statically over the waves, so a grid of the resident count
+// leaves every wave one round of jobs.
+constexpr unsigned kCrcGrid = 512;
+
+// Whether a launch combines each record's stripes inside one workgroup
+// (crc_records_kernel, one launch, no partials in memory): when a record's
+// stripes fit the workgroup's 16 waves and the records still give the chip at
+// least half its waves.
+bool crc_in_group(const CrcPlan& plan, int64_t n_records) {
+    return plan.stripes <= kCrcWaves && n_records * plan.stripes >= kCrcResidentWaves / 2;
+}
+
+// Queue the launches of out[i] = CRC32C of record i; `partial` (plan.stripes
+// words per record) is used unless the stripes combine in their workgroup.
+void launch_crc32c(const void* records, uint64_t record_bytes, uint64_t record_pitch, int64_t n_records,
+                   uint32_t prior, uint32_t* out, uint32_t* partial, const CrcPlan& plan, hipStream_t s) {
+    const bool aligned = (reinterpret_cast<uintptr_t>(records) % 16 == 0) && (record_pitch % 16 == 0) &&
+                         (record_bytes % 16 == 0);
+    const int64_t jobs = n_records * plan.stripes;
+    if (jobs > (int64_t(1) << 31)) throw std::runtime_error("CRC32C: too many records in one call");
+    const auto* base = static_cast<const uint8_t*>(records);
+    CrcStripePowers powers;
+    const uint64_t stripe_bytes = static_cast<uint64_t>(plan.groups) * kCrcGroup;
+    for (int i = 0; i < 6; ++i) powers.p[i] = host_xpow8n(stripe_bytes << i);
+    const uint32_t init_term = host_shift(~prior, record_bytes);
+    if (crc_in_group(plan, n_records)) {
+        const int64_t per_group = kCrcWaves / plan.stripes;
+        const unsigned grid = grid_for((n_records + per_group - 1) / per_group, kCrcGrid);
+        const int stripes = static_cast<int>(plan.stripes);
+        if (aligned)
+            hipLaunchKernelGGL(crc_records_kernel<true>, dim3(grid), dim3(kCrcThreads), 0, s, base, record_pitch,
+                               n_records, stripes, plan.groups, plan.pad, powers, init_term, out);
+        else
+            hipLaunchKernelGGL(crc_records_kernel<false>, dim3(grid), dim3(kCrcThreads), 0, s, base, record_pitch,
+                               n_records, stripes, plan.groups, plan.pad, powers, init_term, out);
+        check_launch("crc32c records");
+        return;
+    }
+    if (!partial) throw std::runtime_error("CRC32C workspace missing");
+    const unsigned grid = grid_for((jobs + kCrcWaves - 1) / kCrcWaves, kCrcGrid);
+    if (aligned)
+        hipLaunchKernelGGL(crc_stripes_kernel<true>, dim3(grid), dim3(kCrcThreads), 0, s, base, record_pitch,
+                           n_records, plan.stripes, plan.groups, plan.pad, partial);
+    else
+        hipLaunchKernelGGL(crc_stripes_kernel<false>, dim3(grid), dim3(kCrcThreads), 0, s, base, record_pitch,
+                           n_records, plan.stripes, plan.groups, plan.pad, partial);
+    check_launch("crc32c stripes");
+    hipLaunchKernelGGL(crc_combine_kernel, dim3(static_cast<unsigned>((n_records + 3) / 4)), dim3(256), 0, s, partial,
+                       n_records, static_cast<int>(plan.stripes), powers, init_term, out);
+    check_launch("crc32c combine");
 }
 
 }  // namespace
@@ -1359,24 +1625,8 @@ int kvsnap_crc32c_records(const void* records, uint64_t record_bytes, uint64_t r
         const size_t need = static_cast<size_t>(plan.stripes) * static_cast<size_t>(n_records) * sizeof(uint32_t);
         if (!workspace || workspace_bytes < need) throw std::runtime_error("CRC32C workspace too small");
         ensure_crc_tables();
-        hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-        const bool aligned = (reinterpret_cast<uintptr_t>(records) % 16 == 0) && (record_pitch % 16 == 0) &&
-                             (record_bytes % 16 == 0);
-        const unsigned grid = grid_for(n_records * plan.stripes, kCrcGrid);
-        auto* partial = static_cast<uint32_t*>(workspace);
-        const auto* base = static_cast<const uint8_t*>(records);
-        if (aligned)
-            hipLaunchKernelGGL(crc_stripes_kernel<true>, dim3(grid), dim3(kCrcThreads), 0, s, base, record_pitch,
-                               n_records, plan.stripes, plan.groups, plan.pad, partial);
-        else
-            hipLaunchKernelGGL(crc_stripes_kernel<false>, dim3(grid), dim3(kCrcThreads), 0, s, base, record_pitch,
-                               n_records, plan.stripes, plan.groups, plan.pad, partial);
-        check_launch("crc32c stripes");
-        const uint32_t stripe_shift = host_xpow8n(static_cast<uint64_t>(plan.groups) * kCrcGroup);
-        const uint32_t init_term = host_shift(~prior, record_bytes);
-        hipLaunchKernelGGL(crc_combine_kernel, dim3(static_cast<unsigned>((n_records + 63) / 64)), dim3(64), 0, s,
-                           partial, n_records, plan.stripes, stripe_shift, init_term, out);
-        check_launch("crc32c combine");
+        launch_crc32c(records, record_bytes, record_pitch, n_records, prior, out, static_cast<uint32_t*>(workspace),
+                      plan, reinterpret_cast<hipStream_t>(stream));
     });
 }
 
