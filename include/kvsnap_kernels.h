@@ -126,6 +126,21 @@ size_t kvsnap_crc32c_workspace_bytes(uint64_t record_bytes, int64_t n_records);
 int kvsnap_crc32c_records(const void* records, uint64_t record_bytes, uint64_t record_pitch, int64_t n_records,
                           uint32_t prior, uint32_t* out, void* workspace, size_t workspace_bytes, uintptr_t stream);
 
+/* The CRC32C of kvsnap_crc32c_records with no allocation at all: no workspace
+ * argument, and no hipMalloc, hipFree or allocating library call.  No
+ * counterpart in the reference; for callers that cannot allocate (code under
+ * HIP graph capture, tight serving loops, harnesses that forbid it).  When a
+ * record's stripes do not combine inside their workgroup (few records), their
+ * partial CRCs go to one static device array of 65536 words (256 KiB) per
+ * GPU, held until the process ends: at most 65536 records per call (a larger
+ * batch fails with an error before anything is queued).  Calls that overlap
+ * on one GPU race on that array, so callers order them (one stream, or
+ * events).  The array keeps the last call's partials; a call reads only what
+ * it has written.  The first call on a device uploads the CRC tables and
+ * looks up the array's address (synchronous), so make one before capturing. */
+int kvsnap_crc32c_records_noalloc(const void* records, uint64_t record_bytes, uint64_t record_pitch,
+                                  int64_t n_records, uint32_t prior, uint32_t* out, uintptr_t stream);
+
 /* out[32 * i .. 32 * i + 31] = SHA-256 digest of record i (16-byte aligned
  * `out`).  Replaces hashlib.sha256(record) at kvsnap/connector/volatile.py:151
  * and kvsnap/store/store.py:622 (the blob id, blobs.py:33-36). */

@@ -1431,6 +1431,29 @@ void launch_crc32c(const void* records, uint64_t record_bytes, uint64_t record_p
     check_launch("crc32c combine");
 }
 
+// The no-allocation entry point's workspace: one array per device, holding
+// the stripes' partial CRCs of one call.  Its address on each device is
+// looked up once (hipGetSymbolAddress) with that device current.
+constexpr int64_t kStaticCrcPartials = 65536;  // 256 KiB
+constexpr int64_t kStaticCrcMaxRecords = kStaticCrcPartials;
+__device__ __align__(256) uint32_t scratch[kStaticCrcPartials];
+uint32_t* g_scratch_ptr[64];
+
+uint32_t* static_crc_workspace() {
+    int device = 0;
+    if (hipGetDevice(&device) != hipSuccess || device < 0 || device >= 64)
+        throw std::runtime_error("no current HIP device for the CRC32C workspace");
+    std::lock_guard<std::mutex> lock(g_table_mutex);
+    if (!g_scratch_ptr[device]) {
+        void* ptr = nullptr;
+        const hipError_t rc = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+        if (rc != hipSuccess || !ptr)
+            throw std::runtime_error(std::string("CRC32C static workspace address: ") + hipGetErrorString(rc));
+        g_scratch_ptr[device] = static_cast<uint32_t*>(ptr);
+    }
+    return g_scratch_ptr[device];
+}
+
 }  // namespace
 
 extern "C" {
@@ -1627,6 +1650,23 @@ int kvsnap_crc32c_records(const void* records, uint64_t record_bytes, uint64_t r
         ensure_crc_tables();
         launch_crc32c(records, record_bytes, record_pitch, n_records, prior, out, static_cast<uint32_t*>(workspace),
                       plan, reinterpret_cast<hipStream_t>(stream));
+    });
+}
+
+int kvsnap_crc32c_records_noalloc(const void* records, uint64_t record_bytes, uint64_t record_pitch,
+                                 int64_t n_records, uint32_t prior, uint32_t* out, uintptr_t stream) {
+    return guard([&] {
+        if (n_records < 0) throw std::runtime_error("negative record count");
+        if (n_records == 0) return;
+        if (n_records > kStaticCrcMaxRecords)
+            throw std::runtime_error("CRC32C without allocation: at most 65536 records per call");
+        if (!out || (!records && record_bytes)) throw std::runtime_error("CRC32C needs device pointers");
+        const CrcPlan plan = crc_plan(record_bytes, n_records, kStaticCrcPartials);
+        if (plan.stripes * n_records > kStaticCrcPartials)
+            throw std::runtime_error("CRC32C without allocation: the static workspace is too small");
+        ensure_crc_tables();
+        launch_crc32c(records, record_bytes, record_pitch, n_records, prior, out, static_crc_workspace(), plan,
+                      reinterpret_cast<hipStream_t>(stream));
     });
 }
 
