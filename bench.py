@@ -957,13 +957,14 @@ def run_ttft(args):
     tier = HostTier(plane, 2 * total)
     worker = KvsnapWorker(plane, host_tier=tier, blobs=BlobDirectory(root))
 
-    def until(condition, seconds=60):
+    def until(condition, seconds=60, finished=()):
         deadline = time.perf_counter() + seconds
         while not condition():
             if time.perf_counter() > deadline:
                 raise RuntimeError("the worker did not report in time")
             worker.bind_connector_metadata(KvsnapMetadata())
-            worker.get_finished(set())
+            worker.get_finished(set(finished))
+            worker.clear_connector_metadata()
             time.sleep(1e-4)
 
     # Turn end: both saves handed off after the step's kernels, fenced, hashed on the GPU, kept.
@@ -972,7 +973,7 @@ def run_ttft(args):
         Transfer("disk", source, durability="durable", num_kv_tokens=tokens)]))
     worker.wait_for_save()
     saved = {}
-    until(lambda: not worker.save_jobs)
+    until(lambda: not worker._saves, finished={"host", "disk"})    # fenced, reported, and booked
     meta = worker.build_connector_worker_meta()
     if meta.errors:
         raise RuntimeError(f"turn-end saves failed: {meta.errors}")
@@ -1006,12 +1007,12 @@ def run_ttft(args):
                     elapsed = (time.perf_counter() - arrival) * 1e3
                     break
                 if loads:
-                    worker.start_load_kv()             # async loads start after the forward
+                    worker.start_load_kv(None)         # async loads start after the forward
                 torch.cuda.current_stream().synchronize()
                 marks.append(time.perf_counter())
                 runnable = "r" in worker.get_finished(set())[1]
                 step += 1
-            until(lambda: not worker.load_jobs)
+            until(lambda: not worker._loads)
             loaded = worker.build_connector_worker_meta()
             exact = exact and loaded.failed_loads == [] and torch.equal(got, expected)
             if rep:

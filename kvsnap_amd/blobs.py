@@ -73,10 +73,17 @@ class BlobDirectory:
         final = self.path(blob_id)
         size = data[1] if isinstance(data, tuple) else len(data)
         if final.exists():
-            with final.open("rb") as stream:
-                length, checksum = parse_header(stream.read(HEADER.size))
-            if length != size or checksum != crc32c:
-                raise CorruptSnapshotError("existing blob differs from its content id")
+            fd = os.open(final, os.O_RDONLY)
+            try:
+                length, checksum = parse_header(os.pread(fd, HEADER.size, 0))
+                if length != size or checksum != crc32c:
+                    raise CorruptSnapshotError("existing blob differs from its content id")
+                if durable:
+                    # Written earlier without a sync: a durable snapshot now refers to it, so it is made durable
+                    # (the caller syncs the directory entry; reference kvsnap/store/blobs.py:80-92).
+                    os.fdatasync(fd)
+            finally:
+                os.close(fd)
             return False
         temporary = self.blob_dir / f"{blob_id}.{uuid.uuid4().hex}.tmp"
         fd = os.open(temporary, os.O_CREAT | os.O_EXCL | os.O_WRONLY, 0o600)
@@ -111,11 +118,7 @@ class BlobDirectory:
                                     unique.items()))
         self.written = sum(written)
         if durable:
-            fd = os.open(self.blob_dir, os.O_RDONLY | os.O_DIRECTORY)
-            try:
-                os.fsync(fd)
-            finally:
-                os.close(fd)
+            self._sync_directory()
         return [dict(blob_id=blob_id, offset=0, length=data[1] if isinstance(data, tuple) else len(data),
                      first_block=index, nblocks=1, crc32c=crc)
                 for index, (data, (blob_id, crc)) in enumerate(zip(blocks, digests))]
@@ -151,10 +154,14 @@ class BlobDirectory:
         fresh = block_ids[keep:]
         self.gathered_blocks = len(fresh)
         self.written = 0
+        identity = plane.layout_identity
+        if durable and keep:
+            # The kept blobs may have been written without a sync; this durable snapshot refers to them.
+            self._make_durable(segment["blob_id"] for segment in segments)
         if not fresh:
             if fenced is not None:
                 fenced.set()
-            return dict(block_ids=block_ids, num_kv_tokens=num_kv_tokens, segments=segments)
+            return dict(block_ids=block_ids, num_kv_tokens=num_kv_tokens, segments=segments, kv_layout=identity)
         from .dataplane import CopyFailed
         with plane.staging(len(fresh)) as staged:
             digests = []
@@ -168,36 +175,77 @@ class BlobDirectory:
             new = self.write_blocks([(staged.pointer + i * size, size) for i in range(len(fresh))],
                                     digests[0].result(), durable=durable, workers=workers)
         segments += [dict(segment, first_block=keep + segment["first_block"]) for segment in new]
-        return dict(block_ids=block_ids, num_kv_tokens=num_kv_tokens, segments=segments)
+        return dict(block_ids=block_ids, num_kv_tokens=num_kv_tokens, segments=segments, kv_layout=identity)
 
-    def read_prepared_into(self, segments, address, block_bytes, *, first_block=0, workers=8, verify="host"):
-        """pread blocks into packed pinned memory; with ``verify="host"`` CRC-check each one there."""
-        if verify not in ("host", "none"):
-            raise ValueError("verify must be host or none")
-        for index, segment in enumerate(segments, start=first_block):
-            if segment["first_block"] != index or segment["nblocks"] != 1:
-                raise CorruptSnapshotError("noncontiguous prepared block mapping")
+    def _make_durable(self, blob_ids):
+        """fdatasync the blobs ``blob_ids`` and their directory."""
+        for blob_id in set(blob_ids):
+            fd = os.open(self.path(blob_id), os.O_RDONLY)
+            try:
+                os.fdatasync(fd)
+            finally:
+                os.close(fd)
+        self._sync_directory()
+
+    def _sync_directory(self):
+        fd = os.open(self.blob_dir, os.O_RDONLY | os.O_DIRECTORY)
+        try:
+            os.fsync(fd)
+        finally:
+            os.close(fd)
+
+    def _read_plan(self, segments, address, block_bytes, first_block):
+        """(blob path, pinned target, payload offset, length, CRC32C, block index) per segment, after checking
+        that the segments map blocks ``first_block, first_block + 1, ...`` one whole KV block each."""
+        plan = []
+        for position, segment in enumerate(segments):
+            block = first_block + position
+            if segment["first_block"] != block or segment["nblocks"] != 1:
+                raise CorruptSnapshotError(f"noncontiguous block mapping: segment {position} is not block {block}")
             offset, length = segment["offset"], segment["length"]
             if type(offset) is not int or type(length) is not int or offset < 0 or length != block_bytes:
-                raise CorruptSnapshotError("prepared segment does not match the KV block size")
+                raise CorruptSnapshotError(f"segment {position} is not one KV block of the block size "
+                                           f"({block_bytes} bytes)")
+            plan.append((self.path(segment["blob_id"]), address + position * block_bytes, HEADER.size + offset,
+                         length, segment["crc32c"], block))
+        return plan
 
-        def read(item):
-            index, segment = item
-            target = address + index * block_bytes
-            offset, length = segment["offset"], segment["length"]
+    def read_prepared_into(self, segments, address, block_bytes, *, first_block=0, workers=8, verify="host"):
+        """Read a snapshot's blocks from their blob files into packed pinned memory.
+
+        Segment i (block ``first_block + i``) lands at ``address + i *
+        block_bytes``, read by ``workers`` threads under a shared lock on
+        ``<root>/.blob.lock`` (reference ``store.py:686-723``).  Every blob's
+        header is checked and the segment must lie inside its payload; with
+        ``verify="host"`` each block's CRC32C is compared in place (a
+        mismatch raises ``CorruptSnapshotError`` before anything reaches the
+        GPU); ``verify="none"`` leaves the comparison to the caller's GPU check.
+        """
+        if verify not in ("host", "none"):
+            raise ValueError("verify must be host or none")
+        plan = self._read_plan(segments, address, block_bytes, first_block)
+        io = self.io
+
+        def fetch(job):
+            path, target, payload_at, length, crc, block = job
             try:
-                with self.path(segment["blob_id"]).open("rb") as stream:
-                    fd = stream.fileno()
-                    size, _ = parse_header(os.pread(fd, HEADER.size, 0))
-                    if offset + length > size:
-                        raise CorruptSnapshotError("invalid blob header or segment bounds")
-                    self.io.pread_into(fd, target, length, HEADER.size + offset)
-            except (OSError, struct.error) as exc:
-                raise CorruptSnapshotError(f"unreadable blob {segment['blob_id']}: {exc}") from exc
-            if verify == "host" and self.io.crc32c_at(target, length) != segment["crc32c"]:
-                raise CorruptSnapshotError("prepared segment checksum mismatch")
+                fd = os.open(path, os.O_RDONLY)
+            except OSError as exc:
+                raise CorruptSnapshotError(f"unreadable blob {path.name}: {exc}") from exc
+            try:
+                stored, _ = parse_header(io.pread_all(fd, HEADER.size, 0))
+                if payload_at - HEADER.size + length > stored:
+                    raise CorruptSnapshotError(f"block {block} runs past the payload of {path.name}")
+                io.pread_into(fd, target, length, payload_at)
+            except OSError as exc:
+                raise CorruptSnapshotError(f"unreadable blob {path.name}: {exc}") from exc
+            finally:
+                os.close(fd)
+            if verify == "host" and io.crc32c_at(target, length) != crc:
+                raise CorruptSnapshotError(f"block {block} fails its checksum (CRC32C)")
 
-        with (self.root / ".blob.lock").open("a+b") as lock_file:
-            fcntl.flock(lock_file, fcntl.LOCK_SH)
+        with (self.root / ".blob.lock").open("a+b") as lock:
+            fcntl.flock(lock, fcntl.LOCK_SH)
             with ThreadPoolExecutor(max_workers=workers, thread_name_prefix="kvsnap-read") as pool:
-                list(pool.map(read, enumerate(segments)))
+                for _ in pool.map(fetch, plan):
+                    pass

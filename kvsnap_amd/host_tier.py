@@ -33,6 +33,7 @@ import uuid
 
 from .blobs import CorruptSnapshotError
 from .dataplane import CopyFailed, PinnedCapacityError
+from .layout import require_layout
 
 
 def unchanged_prefix(block_ids, previous, block_size):
@@ -207,7 +208,7 @@ class HostTier:
         self.gathered_blocks = len(fresh)
         segments = self.adopt(allocations, ids, reuse=reuse)
         return dict(block_ids=block_ids, num_kv_tokens=num_kv_tokens, segments=segments,
-                    locations=self.locations(segments))
+                    locations=self.locations(segments), kv_layout=plane.layout_identity)
 
     def restore(self, block_ids, snapshot, *, verify=False, progress=None, chunk_bytes=64 << 20):
         """Scatter a held snapshot into ``block_ids``; returns the snapshot as restored there.
@@ -228,6 +229,7 @@ class HostTier:
             raise ValueError("one target block per segment is required")
         if verify not in (False, True, "checked"):
             raise ValueError("verify must be False, True or 'checked'")
+        require_layout(snapshot, self.plane.layout_identity)
         with self.borrow(segments, snapshot["locations"]) as sources:
             if verify == "checked":
                 self.plane.load_scatter_checked(list(block_ids), sources, [s["crc32c"] for s in segments],

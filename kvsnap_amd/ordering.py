@@ -14,13 +14,24 @@ EARLY_REPORT_BYTES = 128 << 20
 
 
 def copy_left(progress):
-    """Bytes of a load not yet known complete, or None until every launch is queued."""
-    if not progress or progress[-1][1]:
-        return None
-    for event, left in reversed(progress):
+    """Bytes of a load not yet known complete, or None while launches are still being queued.
+
+    The launches run in order on one stream, so their events complete in
+    order: the answer is the ``left`` of the last entry known complete,
+    found by bisection over the events (the first entry, ``(None, total)``,
+    counts as complete).
+    """
+    if not progress or progress[-1][1] != 0:
+        return None                   # the last launch, which leaves nothing, is not queued yet
+    known, unknown = 0, len(progress)  # entries before ``unknown`` may be complete; ``known`` is
+    while unknown - known > 1:
+        middle = (known + unknown) // 2
+        event = progress[middle][0]
         if event is None or event.query():
-            return left
-    return None
+            known = middle
+        else:
+            unknown = middle
+    return progress[known][1]
 
 
 def early_report(progress, limit=EARLY_REPORT_BYTES):

@@ -22,12 +22,14 @@ pytestmark = pytest.mark.gpu
 LAYERS, BLOCKS, BLOCK_SIZE = 4, 96, 16
 
 
-def run_until(worker, condition, seconds=60):
-    """Step boundaries (bind, report) until ``condition(sending, receiving)`` holds."""
+def run_until(worker, condition, seconds=60, finished=()):
+    """Step boundaries (bind, report, clear) until ``condition(sending, receiving)`` holds; ``finished`` are
+    the requests vLLM reports finished at each step."""
     deadline = time.monotonic() + seconds
     while time.monotonic() < deadline:
         worker.bind_connector_metadata(KvsnapMetadata())
-        sending, receiving = worker.get_finished(set())
+        sending, receiving = worker.get_finished(set(finished))
+        worker.clear_connector_metadata()
         if condition(sending, receiving):
             return sending, receiving
         torch.cuda.synchronize()
@@ -62,18 +64,19 @@ def test_a_session_saved_and_loaded_through_the_worker_is_what_the_next_forward_
         worker.bind_connector_metadata(KvsnapMetadata(saves=[Transfer("r", source, durability=durability,
                                                                       num_kv_tokens=tokens)]))
         worker.wait_for_save()
-        run_until(worker, lambda sending, receiving: worker.save_jobs == {})
+        run_until(worker, lambda sending, receiving: "r" in sending, finished={"r"})    # the blocks are fenced
+        run_until(worker, lambda sending, receiving: not worker._saves)                 # and the save is booked
         meta = worker.build_connector_worker_meta()
         assert meta.errors == {}
         snapshot = meta.prepared["r"]
-        assert len(snapshot["segments"]) == 40
+        assert len(snapshot["segments"]) == 40 and snapshot["kv_layout"] == plane.layout_identity
 
         # The next turn: load into other blocks; the forward that reads them runs as soon as the
         # load is reported, ordered after the copy on the GPU by the worker's forward waits.
         backing[:, :, dst] = 0
         worker.bind_connector_metadata(KvsnapMetadata(loads=[Transfer("r", target, snapshot=snapshot,
                                                                       durability=durability)]))
-        worker.start_load_kv()
+        worker.start_load_kv(None)
         deadline = time.monotonic() + 60
         while "r" not in worker.get_finished(set())[1]:
             assert time.monotonic() < deadline, "the load was never reported"
@@ -84,7 +87,7 @@ def test_a_session_saved_and_loaded_through_the_worker_is_what_the_next_forward_
         # The snapshot's last block carries zeros past the computed tokens.
         expected[:, :, -1, 16 - 5:] = 0
         assert torch.equal(restored.view(torch.int16), expected.view(torch.int16))
-        run_until(worker, lambda sending, receiving: worker.load_jobs == {})
+        run_until(worker, lambda sending, receiving: not worker._loads)
         loaded = worker.build_connector_worker_meta()
         assert loaded.loaded == ["r"] and loaded.failed_loads == []
         assert worker.get_block_ids_with_load_errors() == set()
@@ -94,12 +97,12 @@ def test_a_session_saved_and_loaded_through_the_worker_is_what_the_next_forward_
         backing[:, :, dst[:3]] = 1
         worker.bind_connector_metadata(KvsnapMetadata(loads=[Transfer("p", target, snapshot=snapshot,
                                                                       durability=durability, skip_blocks=3)]))
-        worker.start_load_kv()
+        worker.start_load_kv(None)
         run_until(worker, lambda sending, receiving: "p" in receiving)
         torch.cuda.synchronize()
         assert bool((backing[:, :, dst[:3]] == 1).all())
         assert torch.equal(backing[:, :, dst[3:]].view(torch.int16), expected[:, :, 3:].view(torch.int16))
-        run_until(worker, lambda sending, receiving: worker.load_jobs == {})
+        run_until(worker, lambda sending, receiving: not worker._loads)
         assert worker.build_connector_worker_meta().failed_loads == []
     finally:
         worker.shutdown()

@@ -19,33 +19,20 @@ from unittest.mock import patch
 import pytest
 
 from kvsnap_amd.dataplane import CudaPool, PinnedCapacityError
+from kvsnap_amd.pool import POOL_SIGNATURES, declare
 
 ROOT = Path(__file__).resolve().parents[1]
 REF_POOL = ROOT / "oracle" / "_ref" / "libkvsnap_pool_fakecuda_ref.so"
 
-API = {
-    "kvsnap_pool_create": ([C.c_size_t, C.c_int], C.c_void_p),
-    "kvsnap_pool_destroy": ([C.c_void_p], None),
-    "kvsnap_pool_close_checked": ([C.c_void_p], C.c_int),
-    "kvsnap_pool_reserve": ([C.c_void_p, C.c_size_t, C.POINTER(C.c_uint64), C.POINTER(C.c_void_p)], C.c_int),
-    "kvsnap_pool_copy": ([C.c_void_p, C.c_uint64, C.c_size_t, C.c_void_p, C.c_size_t, C.c_int, C.c_size_t], C.c_int),
-    "kvsnap_pool_copy_2d": ([C.c_void_p, C.c_uint64, C.c_size_t, C.c_size_t, C.c_void_p, C.c_size_t, C.c_size_t,
-                             C.c_size_t, C.c_int, C.c_size_t], C.c_int),
-    "kvsnap_pool_release": ([C.c_void_p, C.c_uint64], C.c_int),
-    "kvsnap_pool_wait": ([C.c_void_p, C.c_uint64], C.c_int),
-    "kvsnap_pool_ready": ([C.c_void_p, C.c_uint64], C.c_int),
-    "kvsnap_cuda_error": ([], C.c_char_p),
-    "kvsnap_test_pending": ([], C.c_int),
-    "kvsnap_test_fail_next_record": ([], None),
-    "kvsnap_test_fail_next_stream_sync": ([], None),
-}
+# The pool's own entry points as the binding types them, plus the stand-in runtime's fault hooks.
+SIGNATURES = dict(POOL_SIGNATURES, kvsnap_test_pending="int <-", kvsnap_test_fail_next_record="void <-",
+                  kvsnap_test_fail_next_stream_sync="void <-")
 
 
 def _typed(path):
     lib = C.CDLL(str(path))
-    for name, (args, result) in API.items():
-        fn = getattr(lib, name)
-        fn.argtypes, fn.restype = args, result
+    for name, signature in SIGNATURES.items():
+        declare(lib, name, signature)
     return lib
 
 
@@ -65,15 +52,11 @@ def fake_pool_path(tmp_path_factory):
 @pytest.fixture(scope="module")
 def lib(fake_pool_path):
     handle = _typed(fake_pool_path)
-    for name, (args, result) in {"kvsnap_test_fail_next_host_alloc": ([], None),
-                                 "kvsnap_test_map_elsewhere": ([C.c_int], None),
-                                 "kvsnap_test_live_events": ([], C.c_int),
-                                 "kvsnap_test_last_copy_stream": ([], C.c_size_t),
-                                 "kvsnap_test_last_host_flags": ([], C.c_uint),
-                                 "kvsnap_pool_copy_stream": ([C.c_void_p, C.POINTER(C.c_size_t)], C.c_int),
-                                 "kvsnap_pool_abi_version": ([], C.c_int)}.items():
-        fn = getattr(handle, name)
-        fn.argtypes, fn.restype = args, result
+    for name, signature in {"kvsnap_test_fail_next_host_alloc": "void <-", "kvsnap_test_map_elsewhere": "void <- int",
+                            "kvsnap_test_live_events": "int <-", "kvsnap_test_last_copy_stream": "size <-",
+                            "kvsnap_test_last_host_flags": "u32 <-",
+                            "kvsnap_pool_copy_stream": "int <- ptr size*"}.items():
+        declare(handle, name, signature)
     return handle
 
 
@@ -304,172 +287,175 @@ def test_pinned_allocation_reads_writes_zeroes_and_bounds(lib, fake_pool_path):
         pool.close()
 
 
-# ---------------------------------------------------------------- Python lifetime with a blocking ABI
+# ---------------------------------------------------------------- Python lifetime, against a scripted library
 
 
-class Function:
-    def __init__(self, implementation):
-        self.implementation = implementation
+class Entry:
+    """One entry point of the scripted library: callable, and typeable as ctypes functions are."""
+
+    def __init__(self, body):
+        self.body, self.argtypes, self.restype = body, None, None
 
     def __call__(self, *args):
-        return self.implementation(*args)
+        return self.body(*args)
 
 
-class BlockingABI:
-    """A stand-in ABI whose copy blocks until released, to race close against it."""
+class ScriptedPool:
+    """The pool C-ABI answered in Python, to drive the binding's lifetime rules without a runtime.
+
+    One pool (handle 101) and one allocation (id 7 at address 128).  A copy
+    stops at a gate until the test opens it, and records whether the pool or
+    the allocation went away while it was inside.
+    """
+
+    HANDLE = 101
 
     def __init__(self):
-        self.entered, self.proceed = threading.Event(), threading.Event()
-        self.destroyed = self.released = self.fail_close = False
-        self.kvsnap_pool_abi_version = Function(lambda: 2)
-        self.kvsnap_cuda_error = Function(lambda: b"stand-in error")
-        self.kvsnap_pool_create = Function(lambda capacity, device: 101)
-        self.kvsnap_pool_destroy = Function(lambda pool: setattr(self, "destroyed", True))
-        self.kvsnap_pool_close_checked = Function(self.close_checked)
-        self.kvsnap_pool_reserve = Function(self.reserve)
-        self.kvsnap_pool_copy = Function(self.copy)
-        self.kvsnap_pool_copy_2d = Function(self.copy)
-        self.kvsnap_pool_wait = Function(lambda pool, allocation: 0)
-        self.kvsnap_pool_ready = Function(lambda pool, allocation: 1)
-        self.kvsnap_pool_release = Function(self.release)
+        self.inside, self.gate = threading.Event(), threading.Event()
+        self.gone = {"pool": False, "allocation": False}
+        self.close_result, self.violations = 0, []
+        self.set(kvsnap_pool_abi_version=lambda: 2, kvsnap_cuda_error=lambda: b"scripted failure",
+                 kvsnap_pool_create=lambda capacity, device: self.HANDLE, kvsnap_pool_destroy=lambda pool: None,
+                 kvsnap_pool_close_checked=self._close, kvsnap_pool_reserve=self._reserve,
+                 kvsnap_pool_copy=self._copy, kvsnap_pool_copy_2d=self._copy,
+                 kvsnap_pool_wait=lambda pool, ident: 0, kvsnap_pool_ready=lambda pool, ident: 1,
+                 kvsnap_pool_release=self._release)
 
-    def close_checked(self, pool):
-        if self.fail_close:
-            return -1
-        self.destroyed = True
+    def set(self, **bodies):
+        for name, body in bodies.items():
+            setattr(self, name, Entry(body))
+
+    def _close(self, pool):
+        if self.close_result == 0:
+            self.gone["pool"] = True
+        return self.close_result
+
+    def _reserve(self, pool, size, ident, pointer):
+        C.cast(ident, C.POINTER(C.c_uint64)).contents.value = 7
+        C.cast(pointer, C.POINTER(C.c_void_p)).contents.value = 128
         return 0
 
-    def reserve(self, pool, size, ident, pointer):
-        C.cast(ident, C.POINTER(C.c_uint64))[0] = 7
-        C.cast(pointer, C.POINTER(C.c_void_p))[0] = 128
+    def _release(self, pool, ident):
+        self.gone["allocation"] = True
         return 0
 
-    def release(self, pool, allocation):
-        self.released = True
-        return 0
-
-    def copy(self, *args):
-        self.entered.set()
-        if not self.proceed.wait(3):
-            raise RuntimeError("copy gate timed out")
-        if self.destroyed or self.released:
-            raise AssertionError("native lifetime ended during an active copy")
+    def _copy(self, *args):
+        self.inside.set()
+        if not self.gate.wait(5):
+            self.violations.append("the gate was never opened")
+        if any(self.gone.values()):
+            self.violations.append(f"ended inside a copy: {self.gone}")
         return 0
 
 
-def _pool_with(abi):
-    with patch("kvsnap_amd.dataplane.C.CDLL", return_value=abi):
+def binding_over(library):
+    """A CudaPool whose library is ``library`` (ctypes loading intercepted)."""
+    with patch.object(C, "CDLL", return_value=library):
         return CudaPool(4096)
 
 
-@pytest.mark.parametrize("strided,close_pool", [(False, True), (True, False)])
-def test_close_waits_for_an_inflight_copy(strided, close_pool):
-    abi = BlockingABI()
-    pool = _pool_with(abi)
+@pytest.mark.parametrize("shape,closing", [("flat", "pool"), ("strided", "allocation")])
+def test_closing_waits_for_a_copy_in_flight(shape, closing):
+    library = ScriptedPool()
+    pool = binding_over(library)
     allocation = pool.reserve(128)
-    errors, closed = [], threading.Event()
+    finished = threading.Event()
+    failures = []
 
-    def copy():
-        try:
-            if strided:
-                allocation.copy_2d(256, 64, 0, 64, 64, 2, to_host=True)
-            else:
-                allocation.copy(256, 128, to_host=True)
-        except BaseException as exc:
-            errors.append(exc)
+    def in_thread(work, done=None):
+        def run():
+            try:
+                work()
+            except BaseException as exc:
+                failures.append(exc)
+            finally:
+                if done is not None:
+                    done.set()
+        thread = threading.Thread(target=run)
+        thread.start()
+        return thread
 
-    def close():
-        try:
-            (pool.close if close_pool else allocation.close)()
-        except BaseException as exc:
-            errors.append(exc)
-        finally:
-            closed.set()
-
-    copier, closer = threading.Thread(target=copy), threading.Thread(target=close)
-    copier.start()
-    assert abi.entered.wait(2)
-    closer.start()
-    try:
-        assert not closed.wait(0.05), "close returned while a copy still borrowed the pool"
-    finally:
-        abi.proceed.set()
-        copier.join(2)
-        closer.join(2)
-        pool.close()
-    assert errors == []
-
-
-def test_failed_wait_and_release_keep_owners_alive():
-    abi = BlockingABI()
-    pool = _pool_with(abi)
-    allocation = pool.reserve(128)
-    tensor = type("Storage", (), {})()
-    allocation._tensor_references = [tensor]
-    allocation_ref, tensor_ref = weakref.ref(allocation), weakref.ref(tensor)
-    abi.kvsnap_pool_wait = Function(lambda pool, allocation: -1)
-    abi.kvsnap_pool_release = Function(lambda pool, allocation: -1)
-    with pytest.raises(RuntimeError):
-        allocation.wait()
-    with pytest.raises(RuntimeError):
-        allocation.close()
-    del allocation, tensor
-    gc.collect()
-    try:
-        assert allocation_ref() is not None and tensor_ref() is not None
-        abi.kvsnap_pool_release = Function(abi.release)
-        allocation_ref().close()
-        gc.collect()
-        assert tensor_ref() is None and allocation_ref() is None
-    finally:
-        pool.close()
-
-
-def test_failed_pool_close_keeps_handle_and_references_for_retry():
-    abi = BlockingABI()
-    pool = _pool_with(abi)
-    allocation = pool.reserve(128)
-    marker = object()
-    allocation._tensor_references = [marker]
-    abi.fail_close = True
-    with pytest.raises(RuntimeError):
-        pool.close()
-    assert pool.handle == 101 and not abi.destroyed and allocation._tensor_references == [marker]
-    abi.fail_close = False
+    copy = (lambda: allocation.copy(256, 128, to_host=True)) if shape == "flat" else \
+        (lambda: allocation.copy_2d(256, 64, 0, 64, 64, 2, to_host=True))
+    copier = in_thread(copy)
+    assert library.inside.wait(2)
+    closer = in_thread(pool.close if closing == "pool" else allocation.close, finished)
+    held = not finished.wait(0.05)
+    library.gate.set()
+    copier.join(3)
+    closer.join(3)
     pool.close()
-    assert pool.handle is None
+    assert held, "close returned while a copy was still inside the library"
+    assert failures == [] and library.violations == []
 
 
-def test_incompatible_abi_is_rejected_before_a_pool_is_created():
-    abi = BlockingABI()
-    abi.kvsnap_pool_abi_version = Function(lambda: 1)
+def test_owners_stay_alive_until_a_wait_or_release_succeeds():
+    library = ScriptedPool()
+    pool = binding_over(library)
+    allocation = pool.reserve(128)
+    owner = type("Owner", (), {})()
+    allocation._tensor_references = [owner]
+    watch_allocation, watch_owner = weakref.ref(allocation), weakref.ref(owner)
+    library.set(kvsnap_pool_wait=lambda pool, ident: -1, kvsnap_pool_release=lambda pool, ident: -1)
+    with pytest.raises(RuntimeError, match="scripted failure"):
+        allocation.wait()
+    with pytest.raises(RuntimeError, match="scripted failure"):
+        allocation.close()
+    del allocation, owner
+    gc.collect()
+    assert watch_allocation() is not None and watch_owner() is not None    # the pool keeps both
+    library.set(kvsnap_pool_release=lambda pool, ident: 0)
+    watch_allocation().close()
+    gc.collect()
+    assert watch_owner() is None and watch_allocation() is None
+    pool.close()
+
+
+def test_a_failed_pool_close_can_be_retried_with_everything_in_place():
+    library = ScriptedPool()
+    pool = binding_over(library)
+    allocation = pool.reserve(128)
+    owner = object()
+    allocation._tensor_references = [owner]
+    library.close_result = -1
+    with pytest.raises(RuntimeError):
+        pool.close()
+    assert (pool.handle, library.gone["pool"], allocation._tensor_references) == (ScriptedPool.HANDLE, False, [owner])
+    library.close_result = 0
+    pool.close()
+    assert pool.handle is None and allocation.closed and allocation._tensor_references == []
+
+
+def test_another_abi_version_is_refused_before_any_pool_exists():
+    library = ScriptedPool()
     created = []
-    abi.kvsnap_pool_create = Function(lambda *a: created.append(a) or 101)
+    library.set(kvsnap_pool_abi_version=lambda: 1,
+                kvsnap_pool_create=lambda capacity, device: created.append(capacity) or ScriptedPool.HANDLE)
     with pytest.raises(RuntimeError, match="unsupported.*ABI"):
-        _pool_with(abi)
+        binding_over(library)
     assert created == []
 
 
-def test_pools_refuse_use_after_fork():
-    abi = BlockingABI()
-    pool = _pool_with(abi)
-    pool._pid = -1
-    with pytest.raises(RuntimeError, match="fork"):
-        pool.reserve(1)
-    with pytest.raises(RuntimeError, match="fork"):
-        pool.close()
-    pool._pid = os.getpid()
+def test_a_forked_child_may_not_touch_the_pool():
+    pool = binding_over(ScriptedPool())
+    owner_pid = pool._pid
+    pool._pid = owner_pid + 1          # as seen from a child: the pool belongs to another process
+    for call in (lambda: pool.reserve(1), pool.close):
+        with pytest.raises(RuntimeError, match="fork"):
+            call()
+    pool._pid = owner_pid
     pool.close()
 
 
-def test_capacity_message_maps_to_pinned_capacity_error():
-    abi = BlockingABI()
-    abi.kvsnap_pool_reserve = Function(lambda *a: -1)
-    abi.kvsnap_cuda_error = Function(lambda: b"pinned capacity exhausted")
-    pool = _pool_with(abi)
+def test_only_the_capacity_message_becomes_pinned_capacity_error():
+    library = ScriptedPool()
+    message = [b"pinned capacity exhausted: 64 bytes free"]
+    library.set(kvsnap_pool_reserve=lambda *args: -1, kvsnap_cuda_error=lambda: message[0])
+    pool = binding_over(library)
     with pytest.raises(PinnedCapacityError):
         pool.reserve(1)
-    abi.kvsnap_cuda_error = Function(lambda: b"other failure")
-    with pytest.raises(RuntimeError, match="other failure"):
+    message[0] = b"some other failure"
+    with pytest.raises(RuntimeError, match="some other failure") as raised:
         pool.reserve(1)
+    assert not isinstance(raised.value, PinnedCapacityError)
     pool.close()
