@@ -61,6 +61,7 @@ import threading
 import time
 
 HBM_PEAK_GBPS = 8000.0
+LATENCY_SAMPLES = 20
 # MI355X's host link, PCIe 5.0 x16: 32 GT/s x 16 lanes, 128b/130b encoding, per direction.
 PCIE5_X16_GBPS = round(32 * 16 * 128 / 130 / 8, 2)
 # SHA-256 runs one dependency chain per record (two lanes of a round wave).
@@ -123,57 +124,155 @@ def link_peaks(torch, staged, stream, nbytes):
     return nbytes / h2d_ms / 1e6, nbytes / d2h_ms / 1e6
 
 
-def cpu_baseline(layers, span, seconds_budget=20.0):
-    """The reference's CPU path restated by the oracle, on this host's cores.
+def host_threads():
+    """(os.cpu_count(), CPUs this process may run on, threads the baseline uses).  A one-GPU box gives a
+    process a share of 16 CPUs whatever the machine has, so the widest leg runs on at most 16 threads."""
+    count = os.cpu_count() or 1
+    allowed = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else count
+    return count, allowed, max(1, min(16, allowed))
 
-    Per sample block: gather its spans into a packed record (memcpy), CRC32C
-    (SSE4.2) and SHA-256 (SHA extensions) of the record, and scatter it back
-    into other blocks (memcpy) -- on 1 thread and on min(16, nproc) threads.
-    Sample: 64 blocks of a 256-block host cache, repeated for about
-    ``seconds_budget`` seconds.
+
+def _timed(fn, seconds):
+    """Best of repeated calls of ``fn`` (at least two, for about ``seconds``), in seconds per call."""
+    best, spent, calls = float("inf"), 0.0, 0
+    while calls < 2 or spent < seconds:
+        t0 = time.perf_counter()
+        fn()
+        took = time.perf_counter() - t0
+        best, spent, calls = min(best, took), spent + took, calls + 1
+    return best
+
+
+def cpu_baseline(layers, span, records=512, seconds_per_leg=0.6):
+    """The reference's CPU path for the default snapshot, on this host's cores, leg by leg.
+
+    The snapshot: ``records`` records of ``layers`` x ``span`` bytes, gathered
+    from seeded random blocks of a host cache of ``2 * records`` blocks (the
+    default workload's 512 records of 2,359,296 B: 1.21 GB).  Legs, each in GB/s
+    of record bytes and ms for the snapshot:
+
+    * gather / scatter: per-(layer, block) memcpy between the cache and
+      packed records (the oracle's restatement of ``dataplane.py:388-437``);
+    * crc32c: the SSE4.2 CRC32C of every record (``io.cpp:16-47``);
+    * sha256: SHA-256 of every record with the SHA extensions (hashlib's role
+      at ``store.py:621-622``, ``volatile.py:229-232``);
+    * pread: the records read back from a page-cached file into host memory
+      by reader threads, each taking one record at a time and checking its
+      CRC32C (``read_prepared_into``, ``store.py:686-723``), through the
+      reference's own compiled ``io.cpp`` pool when ``oracle/_ref`` holds it.
+
+    Each leg runs on 1 thread, on 8 (the reference's hash and read pools) and
+    on the host's share ``N`` (``host_threads``).  ``value``: save + restore
+    bytes over gather + CRC32C + SHA-256 + scatter at ``N`` threads.
     """
+    import concurrent.futures
+    import ctypes as C
     import numpy as np
     import oracle
     oracle.build()
     oracle.sha256_select(True)
     lib = oracle.lib()
-    host_blocks, sample = 256, 64
+    count, allowed, widest = host_threads()
     record = layers * span
-    cache = np.frombuffer(np.random.default_rng(0).bytes(layers * host_blocks * span), dtype=np.uint8).copy()
+    host_blocks = 2 * records
+    rng = np.random.default_rng(0)
+    cache = np.empty(layers * host_blocks * span, dtype=np.uint8)
+    chunk = rng.integers(0, 256, size=64 << 20, dtype=np.uint8)
+    for at in range(0, cache.size, chunk.size):
+        cache[at:at + chunk.size] = chunk[:cache.size - at]
     base = cache.ctypes.data
     span_base = np.array([base + l * host_blocks * span for l in range(layers)], dtype=np.uint64)
     span_pitch = np.full(layers, span, dtype=np.int64)
-    span_off = np.array([l * span for l in range(layers)], dtype=np.int64)
+    span_off = np.arange(layers, dtype=np.int64) * span
     span_len = np.full(layers, span, dtype=np.int64)
-    ids = np.array(random.Random(1).sample(range(1, host_blocks), sample), dtype=np.int64)
-    taken = set(ids.tolist())
-    dst = np.array(random.Random(2).sample([b for b in range(1, host_blocks) if b not in taken], sample),
-                   dtype=np.int64)
-    records = np.zeros(sample * record, dtype=np.uint8)
-    crcs = np.zeros(sample, dtype=np.uint32)
-    shas = np.zeros((sample, 32), dtype=np.uint8)
-    sources = np.array([records.ctypes.data + i * record for i in range(sample)], dtype=np.uint64)
-    threads_max = max(1, min(16, os.cpu_count() or 1))
-    result = {}
-    for threads in sorted({1, threads_max}):
-        reps, elapsed = 0, 0.0
-        while elapsed < seconds_budget / 2 or reps == 0:
-            t0 = time.perf_counter()
-            lib.oracle_copy_threads(layers, span_base.ctypes.data, span_pitch.ctypes.data, span_off.ctypes.data,
-                                    span_len.ctypes.data, ids.ctypes.data, None, sample, records.ctypes.data, record,
-                                    threads)
-            lib.oracle_digest_records(records.ctypes.data, record, record, sample, crcs.ctypes.data,
-                                      shas.ctypes.data, threads)
-            lib.oracle_copy_threads(layers, span_base.ctypes.data, span_pitch.ctypes.data, span_off.ctypes.data,
-                                    span_len.ctypes.data, dst.ctypes.data, sources.ctypes.data, sample, None, record,
-                                    threads)
-            elapsed += time.perf_counter() - t0
-            reps += 1
-        result[threads] = 2 * sample * record * reps / elapsed / 1e9
-    return {"value": round(result[threads_max], 3), "unit": "GB/s", "cores": threads_max, "kind": "port",
-            "single_thread_gbps": round(result[1], 3),
-            "sample": (f"{sample} blocks x {record} B of a {host_blocks}-block host cache: gather + CRC32C + "
-                       f"SHA-256 + scatter, repeated ~{seconds_budget:.0f} s (save + restore bytes per second)")}
+    order = random.Random(1).sample(range(host_blocks), host_blocks)
+    ids = np.array(order[:records], dtype=np.int64)
+    dst = np.array(order[records:], dtype=np.int64)
+    packed = np.zeros(records * record, dtype=np.uint8)
+    sources = np.arange(records, dtype=np.uint64) * record + packed.ctypes.data
+    crcs = np.zeros(records, dtype=np.uint32)
+    shas = np.zeros((records, 32), dtype=np.uint8)
+    copy_args = (layers, span_base.ctypes.data, span_pitch.ctypes.data, span_off.ctypes.data, span_len.ctypes.data)
+
+    def gather(threads):
+        lib.oracle_copy_threads(*copy_args, ids.ctypes.data, None, records, packed.ctypes.data, record, threads)
+
+    def scatter(threads):
+        lib.oracle_copy_threads(*copy_args, dst.ctypes.data, sources.ctypes.data, records, None, record, threads)
+
+    def crc(threads):
+        lib.oracle_digest_records(packed.ctypes.data, record, record, records, crcs.ctypes.data, None, threads)
+
+    def sha(threads):
+        lib.oracle_digest_records(packed.ctypes.data, record, record, records, None, shas.ctypes.data, threads)
+
+    gather(widest)
+    crc(widest)
+    expected = crcs.copy()
+    ref_path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "oracle", "_ref", "libkvsnap_io_ref.so")
+    ref = C.CDLL(ref_path) if os.path.isfile(ref_path) else None
+    if ref is not None:
+        ref.kvsnap_io_pool_create.argtypes, ref.kvsnap_io_pool_create.restype = [C.c_size_t, C.c_size_t], C.c_void_p
+        ref.kvsnap_io_pool_destroy.argtypes, ref.kvsnap_io_pool_destroy.restype = [C.c_void_p], None
+        ref.kvsnap_io_pool_transfer.argtypes = [C.c_void_p, C.c_int, C.c_void_p, C.c_size_t, C.c_int64, C.c_int,
+                                                C.c_int]
+        ref.kvsnap_io_pool_transfer.restype = C.c_int
+        ref.kvsnap_crc32c_extend.argtypes = [C.c_void_p, C.c_size_t, C.c_uint32]
+        ref.kvsnap_crc32c_extend.restype = C.c_uint32
+    legs = {"gather": gather, "scatter": scatter, "crc32c": crc, "sha256": sha}
+    thread_counts = sorted({1, 8, widest})
+    result = {name: {} for name in list(legs) + ["pread"]}
+    with tempfile.TemporaryDirectory(prefix="kvsnap-cpu-") as folder:
+        path = os.path.join(folder, "records")
+        with open(path, "wb") as f:
+            f.write(memoryview(packed))
+        fd = os.open(path, os.O_RDONLY)
+        try:
+            def pread(threads):
+                pool = ref.kvsnap_io_pool_create(threads, 64 << 20) if ref is not None else None
+
+                def one(i):
+                    at = packed.ctypes.data + i * record
+                    if pool is not None:
+                        code = ref.kvsnap_io_pool_transfer(pool, fd, at, record, i * record, 0, 0)
+                        if code:
+                            raise OSError(code, os.strerror(code))
+                        found = ref.kvsnap_crc32c_extend(at, record, 0)
+                    else:
+                        view = memoryview(packed)[i * record:(i + 1) * record]
+                        if os.preadv(fd, [view], i * record) != record:
+                            raise OSError("short read")
+                        found = oracle.crc32c_at(at, record)
+                    if found != expected[i]:
+                        raise RuntimeError("a record read back fails its CRC32C")
+                try:
+                    with concurrent.futures.ThreadPoolExecutor(threads) as readers:
+                        list(readers.map(one, range(records)))
+                finally:
+                    if pool is not None:
+                        ref.kvsnap_io_pool_destroy(pool)
+
+            legs["pread"] = pread
+            for threads in thread_counts:
+                for name, fn in legs.items():
+                    seconds = _timed(lambda: fn(threads), seconds_per_leg)
+                    result[name][threads] = seconds
+        finally:
+            os.close(fd)
+    total = records * record
+    save_restore = {t: 2 * total / sum(result[n][t] for n in ("gather", "crc32c", "sha256", "scatter")) / 1e9
+                    for t in thread_counts}
+    return {"value": round(save_restore[widest], 3), "unit": "GB/s", "cores": widest, "kind": "port",
+            "nproc": count, "affinity_cpus": allowed, "threads": thread_counts,
+            "legs_gbps": {name: {str(t): round(total / s / 1e9, 3) for t, s in times.items()}
+                          for name, times in result.items()},
+            "legs_ms": {name: {str(t): round(s * 1e3, 2) for t, s in times.items()} for name, times in result.items()},
+            "save_restore_gbps": {str(t): round(v, 3) for t, v in save_restore.items()},
+            "pread_kind": "reference (oracle/_ref io.cpp pool)" if ref is not None else "port (os.preadv)",
+            "sample": (f"the {records}-record snapshot ({records} x {record} B = {total} B) gathered from and "
+                       f"scattered into a {host_blocks}-block host cache; best of repeated runs per leg; pread from "
+                       f"a page-cached file"),
+            "threads_note": "widest leg = min(16, CPUs this process may use): a one-GPU box's CPU share"}
 
 
 def measured_traffic(kernel):
@@ -224,13 +323,15 @@ def run_save_restore(args):
     # checked restore (every block's CRC32C folded in as it is copied, then
     # compared with the save's), none of them carrying timing events (events
     # around each of a restore's 19 launches add 0.24 ms to it).  Then a
-    # restore and a checked restore with every launch timed, for the
-    # early-readiness point and the per-launch kernel times.  Medians of five
-    # (all five reported): in the second and later processes on a box, one
-    # restore launch of the third sample has stalled for 17-44 ms.
-    latency = {"save": [], "hashed": [], "restore": [], "early": [], "checked": []}
+    # restore with every launch timed, for the early-readiness point and for
+    # where a slow restore spent its time: the host's wall clock against the
+    # GPU's span from its first launch's start to its last launch's end, and
+    # the longest launch.  Medians, maxima and nearest-rank p99 over
+    # ``LATENCY_SAMPLES`` samples after one discarded, every sample reported.
+    latency = {"save": [], "hashed": [], "restore": [], "early": [], "checked": [], "timed_restore": [],
+               "timed_restore_gpu_span": [], "timed_restore_longest_launch": []}
     lat_timer = KernelTimer()
-    for i in range(6):
+    for i in range(LATENCY_SAMPLES + 1):
         digests, progress = [], []
         t0 = time.perf_counter()
         plane.save_gather(source, targets, tokens, digests=digests)
@@ -243,6 +344,7 @@ def run_save_restore(args):
         t4 = time.perf_counter()
         plane.timer = lat_timer if i else None
         plane.load_scatter(target, targets, progress=progress)
+        t5 = time.perf_counter()
         plane.load_scatter_checked(target, targets, saved_crcs)
         plane.timer = None
         if i:
@@ -250,9 +352,12 @@ def run_save_restore(args):
             latency["save"].append((t1 - t0) * 1e3)
             latency["hashed"].append((t2 - t0) * 1e3)
             latency["restore"].append((t3 - t2) * 1e3)
+            latency["timed_restore"].append((t5 - t4) * 1e3)
             launches = len(progress) - 1
             pairs = lat_timer.pairs["restore"][-launches:]
             latency["early"].append(pairs[0][0].elapsed_time(pairs[early_launch_index(progress)][1]))
+            latency["timed_restore_gpu_span"].append(pairs[0][0].elapsed_time(pairs[-1][1]))
+            latency["timed_restore_longest_launch"].append(max(a.elapsed_time(b) for a, b in pairs))
     lat = {k: statistics.median(v) for k, v in latency.items()}
     checked_launch_ms = lat_timer.summary()["restore_checked"]["avg_ms"]
 
@@ -339,7 +444,7 @@ def run_save_restore(args):
     del records, work, sha_out
     scatter_achieved = 2 * total / (scatter_ms * 1e6)
     crc_achieved = total / (crc_alone_ms * 1e6)
-    cpu = None if args.no_cpu_baseline else cpu_baseline(layers, 65536, args.cpu_seconds)
+    cpu = None if args.no_cpu_baseline else cpu_baseline(layers, 65536, session, args.cpu_seconds)
     out = {
         "metric": "8k Qwen3-8B KV restore/save GB/s and ms; % of host-link and HBM roofline",
         "value": round(2 * total / (ms_per_step * 1e6), 3),
@@ -370,6 +475,10 @@ def run_save_restore(args):
         "restore_checked_frac_of_h2d": round(total / lat["checked"] / 1e6 / h2d_peak, 4),
         "restore_checked_launch_ms": round(checked_launch_ms, 4),
         "latency_samples_ms": {k: [round(v, 2) for v in vs] for k, vs in latency.items()},
+        "latency_max_ms": {k: round(max(vs), 3) for k, vs in latency.items()},
+        "latency_p99_ms": {k: round(percentile(vs, 99), 3) for k, vs in latency.items()},
+        "latency_median_ms": {k: round(v, 3) for k, v in lat.items()},
+        "streams": plane.stream_report(),
         "h2d_peak_gbps": round(h2d_peak, 2),
         "d2h_peak_gbps": round(d2h_peak, 2),
         "restore_frac_of_h2d": round(total / lat["restore"] / 1e6 / h2d_peak, 4),
@@ -395,12 +504,22 @@ def run_save_restore(args):
         "sha256": {"kernel": "sha256_kernel", "ms": round(sha_alone_ms, 3),
                    "gbps": round(total / (sha_alone_ms * 1e6), 2), "records": session,
                    "in_step_ms": round(sha["avg_ms"], 3),
-                   "issue_roofline": sha_issue_bound(size, session, sha_alone_ms)},
+                   "issue_roofline": sha_issue_bound(size, session, sha_alone_ms),
+                   "cpu_ms_by_threads": cpu["legs_ms"]["sha256"] if cpu else None},
         "parity": {"restore_byte_exact": exact, "digests_bit_exact": digests_exact},
         "cpu_baseline": cpu,
     }
     staged.close()
     plane.close()
+    if not args.no_rotating:
+        # The fifth workload beside this one, in the same line: the 8k cache freed first.
+        del plane, caches, backing, staged, targets, tables
+        torch.cuda.empty_cache()
+        rotating = run_rotating(args, hashed=True)
+        out["rotating_fp8"] = {key: rotating[key] for key in (
+            "metric", "value", "unit", "copy_alone_gbps", "rounds", "record_bytes", "sessions_tokens",
+            "decode_step_ms", "p99_compute_stall_ms", "save_mode", "restore_mode", "restore_programs",
+            "byte_exact", "saves_hashed", "digests_exact", "streams")}
     return out
 
 
@@ -501,8 +620,13 @@ def run_disk_fork(args):
 
 # ---------------------------------------------------------------- rotating fp8 sessions under decode load
 
-def run_rotating(args):
+def run_rotating(args, hashed=None):
+    """Qwen3-1.7B fp8-e4m3 sessions of 1k/2k/4k/8k tokens saved and restored round-robin from a side thread
+    beside a synthetic 16-sequence decode on the compute stream (reference results/resume-phases.json:351,
+    396).  ``hashed`` (default: ``--digests``) has every save compute its CRC32C and SHA-256 on the GPU;
+    the last round's are then checked against the oracle's digests of the records."""
     import torch
+    hashed = args.digests if hashed is None else hashed
     from kvsnap_amd import synth
     from kvsnap_amd.dataplane import TorchBlockDataPlane, _check, kernel_library
 
@@ -576,7 +700,7 @@ def run_rotating(args):
     def rotate(rounds):
         for _ in range(rounds):
             for tokens, src, dst, staged, targets in sessions:
-                plane.save_gather(src, targets, tokens, digests=digests if args.digests else None)
+                plane.save_gather(src, targets, tokens, digests=digests if hashed else None)
                 plane.load_scatter(dst, targets)
                 moved[0] += 2 * len(src) * size
         for d in digests:
@@ -593,7 +717,15 @@ def run_rotating(args):
     worker.join()
     elapsed = time.perf_counter() - t0
     exact = all(same_blocks(torch, caches, src, dst) for _, src, dst, _, _ in sessions)
+    digests_exact = None
+    if hashed:
+        import oracle
+        digests_exact = True
+        for (tokens, src, _, staged, _), found in zip(sessions, digests[-len(sessions):]):
+            crcs, shas = oracle.digest_records(staged.pointer, size, size, len(src), threads=host_threads()[2])
+            digests_exact &= found.result() == [(bytes(h).hex(), int(c)) for h, c in zip(shas, crcs)]
     stalls = [max(0.0, t - base_med) for t in loaded]
+    streams = plane.stream_report()
     for *_, staged, _ in sessions:
         staged.close()
     plane.close()
@@ -609,7 +741,7 @@ def run_rotating(args):
             "p99_compute_stall_ms": round(percentile(stalls, 99), 4),
             "save_mode": plane.save_mode, "restore_programs": plane.restore_programs,
             "restore_mode": plane.restore_mode, "gather_programs": plane.gather_programs, "byte_exact": exact,
-            "saves_hashed": bool(args.digests),
+            "saves_hashed": bool(hashed), "digests_exact": digests_exact, "streams": streams,
             "note": "beside this decode (median / p99 stall): direct saves on 4 workgroups with copy-engine "
                     "restores 41 GB/s (+10 % / 0.17 ms), on 2-3 workgroups 30-36 GB/s (+9 % / 0.11 ms), on 6 "
                     "39 GB/s (0.71 ms); with the in-place restore kernel on 4 workgroups 29 GB/s (+21 % / 0.85 ms); "
@@ -1185,8 +1317,11 @@ def main():
     parser.add_argument("--restore-mode", choices=("kernel", "dma"), default=None,
                         help="duplex, rotating-fp8: how restores cross the link")
     parser.add_argument("--disk-dir", default=None, help="disk-fork, turns, ttft: where the blob files go")
-    parser.add_argument("--cpu-seconds", type=float, default=20.0)
+    parser.add_argument("--cpu-seconds", type=float, default=0.6,
+                        help="save-restore: seconds per leg and thread count of the CPU baseline")
     parser.add_argument("--no-cpu-baseline", action="store_true")
+    parser.add_argument("--no-rotating", action="store_true",
+                        help="save-restore: leave out the rotating fp8 sessions beside a decode")
     args = parser.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: every GPU saves and restores its own KV shard over its own host link, "

@@ -7,12 +7,13 @@ event joins the next forward's waits (reference kvsnap/connector/vllm.py:454-467
 import random
 import time
 
+import numpy as np
 import pytest
 
 torch = pytest.importorskip("torch")
 
 from kvsnap_amd import synth
-from kvsnap_amd.blobs import BlobDirectory
+from kvsnap_amd.blobs import HEADER, BlobDirectory
 from kvsnap_amd.dataplane import TorchBlockDataPlane
 from kvsnap_amd.host_tier import HostTier
 from kvsnap_amd.worker import KvsnapMetadata, KvsnapWorker, Transfer
@@ -39,8 +40,8 @@ def run_until(worker, condition, seconds=60, finished=()):
 
 @pytest.mark.parametrize("durability", ["volatile", "durable"])
 @pytest.mark.parametrize("verify", ["gpu", "host"])
-def test_a_session_saved_and_loaded_through_the_worker_is_what_the_next_forward_reads(hip_library, tmp_path,
-                                                                                      durability, verify):
+def test_a_session_saved_and_loaded_through_the_worker_is_what_the_next_forward_reads(hip_library, oracle_lib,
+                                                                                      tmp_path, durability, verify):
     caches, backing = synth.make_caches(LAYERS, BLOCKS, layout="kv_split")
     plane = TorchBlockDataPlane(caches, BLOCK_SIZE, 256 << 20)
     plane.warm_up()
@@ -71,6 +72,25 @@ def test_a_session_saved_and_loaded_through_the_worker_is_what_the_next_forward_
         snapshot = meta.prepared["r"]
         assert len(snapshot["segments"]) == 40 and snapshot["kv_layout"] == plane.layout_identity
 
+        # The oracle's records of the cache (the last one's tail past the computed tokens zeroed): the
+        # snapshot's segments carry their SHA-256 ids and CRC32Cs, and each blob file (durable) holds one.
+        size = plane.block_bytes
+        host = backing.view(torch.uint8).cpu().numpy().reshape(-1).copy()
+        base = backing.data_ptr()
+        host_spans = [(host.ctypes.data + (s[1] - base), s[2], s[0], s[3]) for s in plane.spans()]
+        records = oracle_lib.gather(host_spans, source, size)
+        oracle_lib.zero_tail(records[-1], plane.layers, tokens % BLOCK_SIZE)
+        crcs, shas = oracle_lib.digest_records(records.ctypes.data, size, size, len(source), threads=4)
+        assert [(s["blob_id"], s["crc32c"]) for s in snapshot["segments"]] == \
+            [(bytes(h).hex(), int(c)) for h, c in zip(shas, crcs)]
+        if durability == "durable":
+            blobs = BlobDirectory(tmp_path)
+            for segment, record in zip(snapshot["segments"], records):
+                raw = blobs.path(segment["blob_id"]).read_bytes()
+                assert raw[HEADER.size + segment["offset"]:][:segment["length"]] == record.tobytes()
+        # What the load must leave: the oracle's scatter of those records into the target blocks.
+        oracle_lib.scatter(host_spans, target, [records.ctypes.data + i * size for i in range(len(target))])
+
         # The next turn: load into other blocks; the forward that reads them runs as soon as the
         # load is reported, ordered after the copy on the GPU by the worker's forward waits.
         backing[:, :, dst] = 0
@@ -87,6 +107,9 @@ def test_a_session_saved_and_loaded_through_the_worker_is_what_the_next_forward_
         # The snapshot's last block carries zeros past the computed tokens.
         expected[:, :, -1, 16 - 5:] = 0
         assert torch.equal(restored.view(torch.int16), expected.view(torch.int16))
+        whole = backing.view(torch.uint8).cpu().numpy().reshape(-1)
+        changed = np.flatnonzero(whole != host)
+        assert changed.size == 0, f"{changed.size} bytes differ from the oracle's scatter, first at {changed[0]}"
         run_until(worker, lambda sending, receiving: not worker._loads)
         loaded = worker.build_connector_worker_meta()
         assert loaded.loaded == ["r"] and loaded.failed_loads == []
