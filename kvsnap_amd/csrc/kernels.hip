@@ -356,54 +356,61 @@ __global__ __launch_bounds__(kThreads) void synth_decode_kernel(const int64_t* _
 // with virtual zero bytes) whose raw CRCs are computed independently and
 // combined; crc32c = ~(shift(~prior, N) ^ R(record)).
 //
-// A stripe is one wave's job: `groups` groups of 4 KiB, lane l folding the 64
-// contiguous bytes at l * 64 of every group (four 16-byte loads; the four
-// loads of a wave together cover the group's lines).  A lane's bytes of one
-// group are one slicing-by-4 chain of 16 dwords, with no step between them,
-// and the lane moves to the next group of its chain with one "advance" of 4
-// lookups.  Two chains per lane (even and odd groups of the stripe) keep two
-// independent lookup streams in flight; a chain's runs are 8 KiB apart, so
-//   acc' = chain(advance(acc), run),   advance(s) = shift(s, 8192 - 64),
-// and the chain itself shifts by the run's 64 bytes.  At the end the odd
-// chain's register is shifted past the group it lacks, each lane's register
-// past the lanes after it (per-lane constants), and the wave's XOR is the
-// stripe's raw CRC.  A combine kernel shifts every stripe to its record's end
-// (one wave per record) and adds the initial value's term.
+// A stripe is one wave's job: `groups` groups of 1 KiB, lane l folding the
+// 16-byte word at l * 16 of every group (one coalesced 16-byte load per lane
+// and group).  A lane keeps 6 chains, chain c taking the stripe's groups c,
+// c + 6, ... (6 loads of a batch in flight, 6 independent lookup streams),
+// so a chain's words are 6 KiB apart:
+//   acc' = advance(acc) ^ R(word),   advance(s) = shift(s, 6144),
+// R(word) the word's raw CRC from a zero register: four slicing-by-4 steps
+// that do not wait for acc, so the advance's lookups go out beside theirs.
+// At the end the chains are combined by Horner's rule in the order of their
+// last groups (shift by one group between them), each lane's register is
+// shifted past the lanes after it (per-lane constants), and the wave's XOR is
+// the stripe's raw CRC.  The stripes of a record are shifted to its end (in
+// the workgroup, or by a combine kernel) and the initial value's term added.
 //
-//   S[i][v] = shift(v, 4 - i)                (slicing-by-4, one dword)
-//   G[k][v] = shift(v << 8k, 8192 - 64)      (a chain's advance)
-//   H[k][v] = shift(v << 8k, 4096)           (the chain behind, one group on)
-//   M[l]    = x^(8 * 64 * (63 - l)) mod P    (lane l's run to the group's end)
+//   S[i][v]  = shift(v, 4 - i)                 (slicing-by-4, one dword)
+//   Gn[i][v] = shift(v << 4i, 6144)            (the advance, by nibbles)
+//   H[k][v]  = shift(v << 8k, 1024)            (the chain behind, one group on)
+//   M[l]     = x^(8 * 16 * (63 - l)) mod P     (lane l's word to the group's end)
 //
-// The lookups are the kernel's cost.  Random 8-bit indices into one shared
-// 1 KiB table put several lanes of a wave on one LDS bank, so every lane
-// reads its own copy of S: entry v of S[i] for lane t sits at byte
-//   4096 + (i / 2) * 65536 + v * 256 + (i % 2) * 128 + (t % 32) * 4,
-// in bank t % 32, and the 32 lanes an LDS pass serves never share a bank.
-// The address is one byte move (v into byte 1 of a per-lane constant; the
-// 4096 rides in the instruction's offset field).  The copies fill 128 KiB of
-// the LDS, so a CU holds one 1024-lane workgroup.  G (4 KiB) stays shared at
-// the front of the LDS; with 64-byte runs it takes 4 of every 68 lookups
-// (with one 16-byte word per lane and group it was 4 of 20, and its bank
-// conflicts were 29 % of the LDS's active cycles).
+// The lookups are the kernel's cost, and random indices into one shared
+// table put several lanes of a wave on one LDS bank.  So every lane reads its
+// own copy of S and of Gn, laid out so that lane t's entries all sit in bank
+// t % 32 and the 32 lanes an LDS pass serves never share a bank:
+//   Gn[i][v] for lane t at byte 4096 + (i / 2) * 4096 + v * 256 + (i % 2) * 128 + (t % 32) * 4,
+//   S[i][v]  for lane t at byte 20480 + (i / 2) * 65536 + v * 256 + (i % 2) * 128 + (t % 32) * 4,
+// after the shared H at byte 0 (every table's base then fits the 16-bit offset field of ds_read).
+// An address is one byte move: v_perm_b32 puts the index (a byte of the
+// state, or of its nibbles spread one per byte) into byte 1 of a per-lane
+// constant holding the lane's column; the page rides in the instruction's
+// offset field.  The advance by nibbles takes 8 lookups where bytes would
+// take 4, but 16 tables of 16 entries fit 32 private copies in 16 KiB, where
+// the byte tables' copies would need 128 KiB more than the LDS has; shared,
+// their conflicts had been 29 % of the LDS's active cycles.  H and the S and
+// Gn copies fill 148 KiB of the LDS, so a CU holds one 1024-lane workgroup,
+// as many waves as 128 registers a lane allow anyway.
 constexpr uint32_t kPoly = 0x82F63B78u;
 constexpr int kCrcThreads = 1024;
 constexpr int kCrcWaves = kCrcThreads / 64;
 constexpr int kCrcRun = 16;                  // bytes one lane folds per group: one 16-byte word
-constexpr int kCrcChains = 8;                // groups per batch, each its own chain
+constexpr int kCrcChains = 6;                // groups per batch, each its own chain
 constexpr bool kCrcNontemporal = true;       // streaming loads
 constexpr int kCrcRunWords = kCrcRun / 16;
 constexpr int kCrcBatchWords = kCrcChains * kCrcRunWords;  // 16-byte loads per lane per batch
 constexpr int kCrcGroup = 64 * kCrcRun;      // one wave's group
 constexpr int kCrcMaxStripes = 64;           // per record: the combine's lanes
 constexpr int kCrcResidentWaves = 256 * kCrcWaves;  // one workgroup per CU
-constexpr int kCrcAdvanceBytes = 4 * 1024;   // G, shared, at LDS byte 0
-constexpr int kCrcPrivateBytes = 2 * 65536;  // the lanes' copies of S, after G
-constexpr int kCrcBehindBytes = 4 * 1024;    // H, shared, after S
+constexpr int kCrcBehindBytes = 4 * 1024;    // H, shared, at LDS byte 0
+constexpr int kCrcAdvanceBytes = 16 * 1024;  // the lanes' copies of Gn, after H
+constexpr int kCrcPrivateBytes = 2 * 65536;  // the lanes' copies of S, after Gn
+constexpr int kCrcGnAt = kCrcBehindBytes / 4;                        // in words
+constexpr int kCrcSAt = (kCrcBehindBytes + kCrcAdvanceBytes) / 4;    // in words
 
-// g_crc_tables: S[4][256], then G[4][256], then H[4][256], then M[64].
+// g_crc_tables: S[4][256], then Gn[8][16], then H[4][256], then M[64].
 constexpr int kCrcAdvance = 4 * 256;
-constexpr int kCrcBehind = kCrcAdvance + 4 * 256;
+constexpr int kCrcBehind = kCrcAdvance + 8 * 16;
 constexpr int kCrcLaneShift = kCrcBehind + 4 * 256;
 constexpr int kCrcTableWords = kCrcLaneShift + 64;
 
@@ -428,14 +435,15 @@ __device__ __forceinline__ uint32_t lds_word(const uint32_t* lds, uint32_t byte)
     return *reinterpret_cast<const uint32_t*>(reinterpret_cast<const char*>(lds) + byte);
 }
 
-// The per-lane address constant: byte 0 = the lane's column in S[0] and S[2],
-// byte 1 = its column in S[1] and S[3], byte 2 = 1 (the second 64 KiB).
+// The per-lane address constant: byte 0 = the lane's column in S[0], S[2] and
+// the even Gn tables, byte 1 = its column in S[1], S[3] and the odd Gn tables,
+// byte 2 = 1 (S's second 64 KiB).
 __device__ __forceinline__ uint32_t crc_columns(uint32_t lane) {
     const uint32_t col = (lane & 31u) * 4u;
     return col | ((col + 128u) << 8) | (1u << 16);
 }
 
-// shift(acc, d) for the distance d its table G (at LDS byte 0) was built for.
+// shift(acc, d) for the distance d of the shared byte tables at `lds` (H).
 __device__ __forceinline__ uint32_t crc_advance(const uint32_t* lds, uint32_t acc) {
     return xor3(lds_word(lds, (acc & 0xFFu) << 2), lds_word(lds, 1024u + (((acc >> 8) & 0xFFu) << 2)),
                 lds_word(lds, 2048u + (((acc >> 16) & 0xFFu) << 2))) ^
@@ -493,70 +501,72 @@ __device__ __forceinline__ void crc_load_any(const uint8_t* __restrict__ rec, in
 }
 
 // One dword through slicing-by-4 looks up the four bytes of x = state ^
-// dword.  v_perm_b32 picks
-// bytes of {S0 = x (bytes 4-7), S1 = cols (bytes 0-3)}, selector 12 giving
-// 0x00: the address of S[i][byte i of x] is byte i of x in byte 1 above the
-// lane's column, one instruction per lookup:
+// dword.  v_perm_b32 picks bytes of {S0 = x (bytes 4-7), S1 = cols (bytes
+// 0-3)}, selector 12 giving 0x00: the address of S[i][byte i of x] is byte i
+// of x in byte 1 above the lane's column, one instruction per lookup:
 //   S[0]: ((x & 0xFF) << 8) | col                    selector 0x0C0C0400
 //   S[1]: (x & 0xFF00) | (col + 128)                  selector 0x0C0C0501
 //   S[2]: 0x10000 | ((x >> 8) & 0xFF00) | col          selector 0x0C020600
 //   S[3]: 0x10000 | ((x >> 16) & 0xFF00) | (col + 128) selector 0x0C020701
-// One slicing-by-4 step of every chain at once: all the chains' lookups are
-// issued before any result is used, so a wave keeps 4 * kCrcChains LDS reads
-// in flight (left to itself the compiler runs the chains one after another,
-// each step waiting out a whole LDS round trip).
-__device__ __forceinline__ void crc_step_all(const uint32_t* lds, uint32_t cols, uint32_t* s, const uint32_t* data) {
-    const uint32_t* tab = lds + kCrcAdvanceBytes / 4;
-    uint32_t r[kCrcChains][4];
-#pragma unroll
-    for (int c = 0; c < kCrcChains; ++c) {
-        const uint32_t x = s[c] ^ data[c];
-        r[c][0] = lds_word(tab, __builtin_amdgcn_perm(x, cols, 0x0C0C0400u));
-        r[c][1] = lds_word(tab, __builtin_amdgcn_perm(x, cols, 0x0C0C0501u));
-        r[c][2] = lds_word(tab, __builtin_amdgcn_perm(x, cols, 0x0C020600u));
-        r[c][3] = lds_word(tab, __builtin_amdgcn_perm(x, cols, 0x0C020701u));
-    }
-    __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-    for (int c = 0; c < kCrcChains; ++c) s[c] = xor3(r[c][0], r[c][1], r[c][2]) ^ r[c][3];
-    __builtin_amdgcn_sched_barrier(0);
+// Every chain's lookups of a step are issued before any result is used, so
+// a wave keeps 4 * kCrcChains LDS reads in flight (left to itself the
+// compiler runs the chains one after another, each step waiting out a whole
+// LDS round trip).
+
+// The advance of one chain, issued: Gn's eight lookups of `x` (nibble 2k is byte k of `lo`, nibble 2k + 1
+// byte k of `hi`; Gn[2k] and Gn[2k + 1] share page k, columns col and col + 128: bytes 0 and 1 of `cols`).
+__device__ __forceinline__ void crc_advance_issue(const uint32_t* lds, uint32_t cols, uint32_t x, uint32_t* r) {
+    const uint32_t lo = x & 0x0F0F0F0Fu, hi = (x >> 4) & 0x0F0F0F0Fu;
+    const uint32_t* gn = lds + kCrcGnAt;
+    r[0] = lds_word(gn, __builtin_amdgcn_perm(lo, cols, 0x0C0C0400u));
+    r[1] = lds_word(gn, __builtin_amdgcn_perm(hi, cols, 0x0C0C0401u));
+    r[2] = lds_word(gn + 1024, __builtin_amdgcn_perm(lo, cols, 0x0C0C0500u));
+    r[3] = lds_word(gn + 1024, __builtin_amdgcn_perm(hi, cols, 0x0C0C0501u));
+    r[4] = lds_word(gn + 2048, __builtin_amdgcn_perm(lo, cols, 0x0C0C0600u));
+    r[5] = lds_word(gn + 2048, __builtin_amdgcn_perm(hi, cols, 0x0C0C0601u));
+    r[6] = lds_word(gn + 3072, __builtin_amdgcn_perm(lo, cols, 0x0C0C0700u));
+    r[7] = lds_word(gn + 3072, __builtin_amdgcn_perm(hi, cols, 0x0C0C0701u));
 }
 
-// Fold a batch: chain c advances to its next run and takes it through slicing-by-4.  Chains past `count`
-// (the last batch's missing groups) are left alone.
+// Fold a batch: chain c takes word v[c], acc' = shift(acc, kCrcChains KiB) ^ R(word), R the word's raw
+// CRC from a zero register in four slicing-by-4 steps.  R does not depend on acc, so the advances' lookups (a
+// quarter of the chains beside each step) ride along with the steps': four LDS round trips per batch, where
+// advancing first and then stepping from the advanced register takes five.  Chains past `count` (the
+// last batch's missing groups) are left alone.
 __device__ __forceinline__ void crc_fold_batch(const uint32_t* lds, uint32_t cols, const u32x4* v, uint32_t* acc,
                                                int count) {
-    uint32_t s[kCrcChains], r[kCrcChains][4];
+    static_assert(kCrcRunWords == 1, "one word per chain and batch");
+    constexpr int kQuarter = (kCrcChains + 3) / 4;
+    const uint32_t* tab = lds + kCrcSAt;
+    uint32_t t[kCrcChains], g[kCrcChains];
 #pragma unroll
-    for (int c = 0; c < kCrcChains; ++c) {
-        r[c][0] = lds_word(lds, (acc[c] & 0xFFu) << 2);
-        r[c][1] = lds_word(lds, 1024u + (((acc[c] >> 8) & 0xFFu) << 2));
-        r[c][2] = lds_word(lds, 2048u + (((acc[c] >> 16) & 0xFFu) << 2));
-        r[c][3] = lds_word(lds, 3072u + ((acc[c] >> 24) << 2));
-    }
-    __builtin_amdgcn_sched_barrier(0);
+    for (int k = 0; k < 4; ++k) {
+        uint32_t r[kCrcChains][4], q[kQuarter][8];
 #pragma unroll
-    for (int c = 0; c < kCrcChains; ++c) s[c] = xor3(r[c][0], r[c][1], r[c][2]) ^ r[c][3];
-    __builtin_amdgcn_sched_barrier(0);
+        for (int c = 0; c < kCrcChains; ++c) {
+            const uint32_t d = k == 0 ? v[c].x : k == 1 ? v[c].y : k == 2 ? v[c].z : v[c].w;
+            const uint32_t x = k == 0 ? d : t[c] ^ d;
+            r[c][0] = lds_word(tab, __builtin_amdgcn_perm(x, cols, 0x0C0C0400u));
+            r[c][1] = lds_word(tab, __builtin_amdgcn_perm(x, cols, 0x0C0C0501u));
+            r[c][2] = lds_word(tab, __builtin_amdgcn_perm(x, cols, 0x0C020600u));
+            r[c][3] = lds_word(tab, __builtin_amdgcn_perm(x, cols, 0x0C020701u));
+        }
 #pragma unroll
-    for (int k = 0; k < kCrcRunWords; ++k) {
-        uint32_t d[kCrcChains];
+        for (int i = 0; i < kQuarter; ++i)
+            if (k * kQuarter + i < kCrcChains) crc_advance_issue(lds, cols, acc[k * kQuarter + i], q[i]);
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-        for (int c = 0; c < kCrcChains; ++c) d[c] = v[c * kCrcRunWords + k].x;
-        crc_step_all(lds, cols, s, d);
+        for (int c = 0; c < kCrcChains; ++c) t[c] = xor3(r[c][0], r[c][1], r[c][2]) ^ r[c][3];
 #pragma unroll
-        for (int c = 0; c < kCrcChains; ++c) d[c] = v[c * kCrcRunWords + k].y;
-        crc_step_all(lds, cols, s, d);
-#pragma unroll
-        for (int c = 0; c < kCrcChains; ++c) d[c] = v[c * kCrcRunWords + k].z;
-        crc_step_all(lds, cols, s, d);
-#pragma unroll
-        for (int c = 0; c < kCrcChains; ++c) d[c] = v[c * kCrcRunWords + k].w;
-        crc_step_all(lds, cols, s, d);
+        for (int i = 0; i < kQuarter; ++i)
+            if (k * kQuarter + i < kCrcChains)
+                g[k * kQuarter + i] =
+                    xor3(xor3(q[i][0], q[i][1], q[i][2]), xor3(q[i][3], q[i][4], q[i][5]), q[i][6]) ^ q[i][7];
+        __builtin_amdgcn_sched_barrier(0);
     }
 #pragma unroll
     for (int c = 0; c < kCrcChains; ++c)
-        if (c < count) acc[c] = s[c];
+        if (c < count) acc[c] = g[c] ^ t[c];
 }
 
 // The batches of one stripe after its first (already in `cur`, `count` groups, folded next), with the
@@ -577,8 +587,8 @@ __device__ __forceinline__ void crc_fold_rest(const uint32_t* lds, uint32_t cols
     }
 }
 
-// The LDS tables of a CRC workgroup: G shared at byte 0, the lanes' private
-// copies of S, then H shared.
+// The LDS tables of a CRC workgroup: H shared at byte 0, then the lanes'
+// private copies of Gn and of S.
 __device__ __forceinline__ void crc_fill_tables(uint32_t* lds) {
     // Thread t owns S entry t (table t / 256, value t % 256): one read, then its 32 lane columns are one
     // 128-byte run of the private layout, written as eight 16-byte stores.
@@ -586,37 +596,53 @@ __device__ __forceinline__ void crc_fill_tables(uint32_t* lds) {
     const uint32_t t = threadIdx.x, table = t >> 8, v = t & 255u;
     const uint32_t word = g_crc_tables[t];
     const u32x4 four = {word, word, word, word};
-    u32x4* run = reinterpret_cast<u32x4*>(reinterpret_cast<char*>(lds) + kCrcAdvanceBytes + (table >> 1) * 65536u +
+    u32x4* run = reinterpret_cast<u32x4*>(reinterpret_cast<char*>(lds + kCrcSAt) + (table >> 1) * 65536u +
                                           v * 256u + (table & 1u) * 128u);
 #pragma unroll
     for (int k = 0; k < 8; ++k) run[k] = four;
-    lds[t] = g_crc_tables[kCrcAdvance + t];
-    lds[(kCrcAdvanceBytes + kCrcPrivateBytes) / 4 + t] = g_crc_tables[kCrcBehind + t];
+    // Eight threads per Gn entry (table e / 16, value e % 16), four lane columns (16 bytes) each.
+    const uint32_t e = t >> 3, nib_table = e >> 4, nib = e & 15u;
+    const uint32_t adv = g_crc_tables[kCrcAdvance + e];
+    *reinterpret_cast<u32x4*>(reinterpret_cast<char*>(lds + kCrcGnAt) + (nib_table >> 1) * 4096u + nib * 256u +
+                              (nib_table & 1u) * 128u + (t & 7u) * 16u) = u32x4{adv, adv, adv, adv};
+    lds[t] = g_crc_tables[kCrcBehind + t];
+}
+
+// Groups of padding only (in stripe 0) are skipped, not folded: the registers are still zero there.
+__device__ __forceinline__ int crc_lead(int64_t start) {
+    return start < 0 ? static_cast<int>((-start) / kCrcGroup) : 0;
+}
+
+// Issue the loads of the first batch of the stripe of `groups` groups at record offset `start` into `a`.
+// Chain c takes groups lead + c, lead + c + kCrcChains, ...  Only the first batch may hold front padding,
+// and only the last may hold fewer groups than chains.
+template <bool kAligned>
+__device__ __forceinline__ void crc_stripe_first(const uint8_t* __restrict__ rec, int64_t start, int groups,
+                                                 uint32_t lane, u32x4* a) {
+    const int g = crc_lead(start);
+    const int count = groups - g < kCrcChains ? groups - g : kCrcChains;
+    const int64_t at = start + static_cast<int64_t>(g) * kCrcGroup;
+    if (kAligned && at >= 0 && count == kCrcChains)
+        crc_load_batch(rec, at, lane, a);
+    else
+        crc_load_any<kAligned>(rec, at, count, lane, a);
 }
 
 // One wave's job: the raw CRC of the stripe of `groups` groups whose first byte is at record offset
-// `start` (negative in the first stripe: front padding), the XOR of the wave's lanes.
+// `start` (negative in the first stripe: front padding), the XOR of the wave's lanes.  The loads of its
+// first batch into `a` were issued by crc_stripe_first, possibly before the tables were filled.
 template <bool kAligned>
-__device__ __forceinline__ uint32_t crc_stripe(const uint32_t* lds, uint32_t lane, uint32_t cols, uint32_t lane_shift,
-                                               const uint8_t* __restrict__ rec, int64_t start, int groups) {
-    const uint32_t* behind_table = lds + (kCrcAdvanceBytes + kCrcPrivateBytes) / 4;
-    // Groups of padding only (in stripe 0) are skipped, not folded: the registers are still zero there.
-    const int lead = start < 0 ? static_cast<int>((-start) / kCrcGroup) : 0;
-    // Chain c takes groups lead + c, lead + c + kCrcChains, ...  Only the first batch may hold front
-    // padding, and only the last may hold fewer groups than chains.
+__device__ __forceinline__ uint32_t crc_stripe_rest(const uint32_t* lds, uint32_t lane, uint32_t cols,
+                                                    uint32_t lane_shift, const uint8_t* __restrict__ rec,
+                                                    int64_t start, int groups, u32x4* a) {
+    const uint32_t* behind_table = lds;
+    const int lead = crc_lead(start);
     uint32_t acc[kCrcChains];
 #pragma unroll
     for (int c = 0; c < kCrcChains; ++c) acc[c] = 0;
-    u32x4 a[kCrcBatchWords], b[kCrcBatchWords];
+    u32x4 b[kCrcBatchWords];
     int g = lead;
     const int count = groups - g < kCrcChains ? groups - g : kCrcChains;
-    {
-        const int64_t at = start + static_cast<int64_t>(g) * kCrcGroup;
-        if (kAligned && at >= 0 && count == kCrcChains)
-            crc_load_batch(rec, at, lane, a);
-        else
-            crc_load_any<kAligned>(rec, at, count, lane, a);
-    }
     // The first batch's loads are complete before the steady state starts, which the wait for its
     // prefetches then counts on (vmcnt(0); expcnt and lgkmcnt left alone).
     __builtin_amdgcn_s_waitcnt(0x0F70);
@@ -679,22 +705,39 @@ __global__ __launch_bounds__(kCrcThreads) void crc_stripes_kernel(const uint8_t*
                                                                  int64_t n_records, int64_t stripes, int groups,
                                                                  uint64_t pad, uint32_t* __restrict__ partial) {
     __shared__ uint32_t lds[(kCrcAdvanceBytes + kCrcPrivateBytes + kCrcBehindBytes) / 4];
-    crc_fill_tables(lds);
     const uint32_t lane = threadIdx.x & 63u;
-    const uint32_t lane_shift = g_crc_tables[kCrcLaneShift + lane];
-    const uint32_t cols = crc_columns(lane);
-    __syncthreads();
     // Jobs, records and stripes fit 32 bits (the host checks): 32-bit job arithmetic keeps the scalar
     // registers free of 64-bit division.
     const uint32_t jobs = static_cast<uint32_t>(n_records) * static_cast<uint32_t>(stripes);
     const uint32_t waves = gridDim.x * kCrcWaves;
     const int64_t stripe_bytes = static_cast<int64_t>(groups) * kCrcGroup;
     const uint32_t first = blockIdx.x * kCrcWaves + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    for (uint32_t job = first; job < jobs; job += waves) {
-        const uint32_t r = job / static_cast<uint32_t>(stripes), j = job - r * static_cast<uint32_t>(stripes);
-        const int64_t start = static_cast<int64_t>(j) * stripe_bytes - static_cast<int64_t>(pad);
-        const uint32_t x = crc_stripe<kAligned>(lds, lane, cols, lane_shift, records + static_cast<int64_t>(r) * pitch,
-                                                start, groups);
+    const auto job_record = [&](uint32_t job) {
+        return records + static_cast<int64_t>(job / static_cast<uint32_t>(stripes)) * pitch;
+    };
+    const auto job_start = [&](uint32_t job) {
+        return static_cast<int64_t>(job % static_cast<uint32_t>(stripes)) * stripe_bytes - static_cast<int64_t>(pad);
+    };
+    uint32_t lane_shift, cols;
+    {
+        // The first job's first batch is in flight while the tables are filled.
+        u32x4 a[kCrcBatchWords];
+        if (first < jobs) crc_stripe_first<kAligned>(job_record(first), job_start(first), groups, lane, a);
+        crc_fill_tables(lds);
+        lane_shift = g_crc_tables[kCrcLaneShift + lane];
+        cols = crc_columns(lane);
+        __syncthreads();
+        if (first < jobs) {
+            const uint32_t x =
+                crc_stripe_rest<kAligned>(lds, lane, cols, lane_shift, job_record(first), job_start(first), groups, a);
+            if (lane == 0) partial[first] = x;
+        }
+    }
+    for (uint32_t job = first + waves; job < jobs; job += waves) {
+        u32x4 a[kCrcBatchWords];
+        crc_stripe_first<kAligned>(job_record(job), job_start(job), groups, lane, a);
+        const uint32_t x = crc_stripe_rest<kAligned>(lds, lane, cols, lane_shift, job_record(job), job_start(job),
+                                                     groups, a);
         if (lane == 0) partial[job] = x;
     }
 }
@@ -704,6 +747,45 @@ __global__ __launch_bounds__(kCrcThreads) void crc_stripes_kernel(const uint8_t*
 // each wave shifts its stripe's raw CRC to the record's end, and the
 // workgroup XORs them in LDS, so no second launch combines them.  For many
 // records (the chip fills with a few stripes each).
+// One round of crc_records_kernel: the records from `base` on.  `a` holds the wave's first batch already
+// in flight when `loaded`.
+template <bool kAligned>
+__device__ __forceinline__ void crc_records_round(const uint32_t* lds, uint32_t* stripe_crc, uint32_t lane,
+                                                  uint32_t cols, uint32_t lane_shift, int wave,
+                                                  const uint8_t* __restrict__ records, uint64_t pitch,
+                                                  int64_t n_records, int stripes, int groups, uint64_t pad,
+                                                  const CrcStripePowers& powers, uint32_t init_term,
+                                                  uint32_t* __restrict__ out, int64_t base, u32x4* a, bool loaded) {
+    const int per_group = kCrcWaves / stripes;
+    const int rec_in_round = wave / stripes, j = wave - rec_in_round * stripes;
+    const int64_t r = base + rec_in_round;
+    if (rec_in_round < per_group && r < n_records) {  // wave-uniform
+        // The wave's stripe is the same every round: hidden here, or what the compiler derives from it
+        // stays live across rounds and the registers spill.
+        int64_t start = static_cast<int64_t>(j) * groups * kCrcGroup - static_cast<int64_t>(pad);
+        asm volatile("" : "+s"(start));
+        if (!loaded) crc_stripe_first<kAligned>(records + r * pitch, start, groups, lane, a);
+        uint32_t x = crc_stripe_rest<kAligned>(lds, lane, cols, lane_shift, records + r * pitch, start, groups, a);
+        const int behind = stripes - 1 - j;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {  // stripes <= 16
+            if ((behind >> i) & 1) {
+                uint32_t power = powers.p[i];
+                asm volatile("" : "+s"(power));  // per round, as for the lane shift
+                x = gf_mul(power, x);
+            }
+        }
+        if (lane == 0) stripe_crc[wave] = x;
+    }
+    __syncthreads();
+    if (threadIdx.x < static_cast<unsigned>(per_group) && base + threadIdx.x < n_records) {
+        uint32_t x = 0;
+        for (int k = 0; k < stripes; ++k) x ^= stripe_crc[threadIdx.x * stripes + k];
+        out[base + threadIdx.x] = ~(init_term ^ x);
+    }
+    __syncthreads();
+}
+
 template <bool kAligned>
 __global__ __launch_bounds__(kCrcThreads) void crc_records_kernel(const uint8_t* __restrict__ records, uint64_t pitch,
                                                                  int64_t n_records, int stripes, int groups,
@@ -711,42 +793,32 @@ __global__ __launch_bounds__(kCrcThreads) void crc_records_kernel(const uint8_t*
                                                                  uint32_t init_term, uint32_t* __restrict__ out) {
     __shared__ uint32_t lds[(kCrcAdvanceBytes + kCrcPrivateBytes + kCrcBehindBytes) / 4];
     __shared__ uint32_t stripe_crc[kCrcWaves];
-    crc_fill_tables(lds);
     const uint32_t lane = threadIdx.x & 63u;
-    const uint32_t lane_shift = g_crc_tables[kCrcLaneShift + lane];
-    const uint32_t cols = crc_columns(lane);
     const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
     const int per_group = kCrcWaves / stripes;
-    const int rec_in_round = wave / stripes, j = wave - rec_in_round * stripes;
-    const int64_t stripe_bytes = static_cast<int64_t>(groups) * kCrcGroup;
-    __syncthreads();
-    for (int64_t base = static_cast<int64_t>(blockIdx.x) * per_group; base < n_records;
-         base += static_cast<int64_t>(gridDim.x) * per_group) {
-        const int64_t r = base + rec_in_round;
-        if (rec_in_round < per_group && r < n_records) {  // wave-uniform
-            // The wave's stripe is the same every round: hidden here, or what the compiler derives from it
-            // stays live across rounds and the registers spill.
-            int64_t start = static_cast<int64_t>(j) * stripe_bytes - static_cast<int64_t>(pad);
-            asm volatile("" : "+s"(start));
-            uint32_t x = crc_stripe<kAligned>(lds, lane, cols, lane_shift, records + r * pitch, start, groups);
-            const int behind = stripes - 1 - j;
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {  // stripes <= 16
-                if ((behind >> i) & 1) {
-                    uint32_t power = powers.p[i];
-                    asm volatile("" : "+s"(power));  // per round, as for the lane shift
-                    x = gf_mul(power, x);
-                }
-            }
-            if (lane == 0) stripe_crc[wave] = x;
-        }
+    const int64_t first = static_cast<int64_t>(blockIdx.x) * per_group;
+    const int64_t stride = static_cast<int64_t>(gridDim.x) * per_group;
+    uint32_t lane_shift, cols;
+    {
+        // The first round's first batch is in flight while the tables are filled.
+        u32x4 a[kCrcBatchWords];
+        const int rec_in_round = wave / stripes, j = wave - rec_in_round * stripes;
+        if (rec_in_round < per_group && first + rec_in_round < n_records)
+            crc_stripe_first<kAligned>(records + (first + rec_in_round) * pitch,
+                                       static_cast<int64_t>(j) * groups * kCrcGroup - static_cast<int64_t>(pad),
+                                       groups, lane, a);
+        crc_fill_tables(lds);
+        lane_shift = g_crc_tables[kCrcLaneShift + lane];
+        cols = crc_columns(lane);
         __syncthreads();
-        if (threadIdx.x < static_cast<unsigned>(per_group) && base + threadIdx.x < n_records) {
-            uint32_t x = 0;
-            for (int k = 0; k < stripes; ++k) x ^= stripe_crc[threadIdx.x * stripes + k];
-            out[base + threadIdx.x] = ~(init_term ^ x);
-        }
-        __syncthreads();
+        if (first < n_records)  // workgroup-uniform
+            crc_records_round<kAligned>(lds, stripe_crc, lane, cols, lane_shift, wave, records, pitch, n_records,
+                                        stripes, groups, pad, powers, init_term, out, first, a, true);
+    }
+    for (int64_t base = first + stride; base < n_records; base += stride) {
+        u32x4 a[kCrcBatchWords];
+        crc_records_round<kAligned>(lds, stripe_crc, lane, cols, lane_shift, wave, records, pitch, n_records,
+                                    stripes, groups, pad, powers, init_term, out, base, a, false);
     }
 }
 
@@ -1268,9 +1340,9 @@ void ensure_crc_tables() {
         const uint32_t m = host_xpow8n(4 - i);
         for (uint32_t v = 0; v < 256; ++v) tables[256 * i + v] = host_gf_mul(m, v);
     }
-    const uint32_t advance = host_xpow8n(static_cast<uint64_t>(kCrcChains) * kCrcGroup - kCrcRun);
-    for (uint32_t k = 0; k < 4; ++k)
-        for (uint32_t v = 0; v < 256; ++v) tables[kCrcAdvance + 256 * k + v] = host_gf_mul(advance, v << (8 * k));
+    const uint32_t advance = host_xpow8n(static_cast<uint64_t>(kCrcChains) * kCrcGroup);
+    for (uint32_t i = 0; i < 8; ++i)
+        for (uint32_t v = 0; v < 16; ++v) tables[kCrcAdvance + 16 * i + v] = host_gf_mul(advance, v << (4 * i));
     const uint32_t behind = host_xpow8n(kCrcGroup);
     for (uint32_t k = 0; k < 4; ++k)
         for (uint32_t v = 0; v < 256; ++v) tables[kCrcBehind + 256 * k + v] = host_gf_mul(behind, v << (8 * k));
@@ -1347,7 +1419,7 @@ struct CrcPlan {
     uint64_t pad;     // virtual zero bytes in front of each record
 };
 
-// Stripes of `groups` 4 KiB groups, the first one padded in front.  A stripe
+// Stripes of `groups` 1 KiB groups, the first one padded in front.  A stripe
 // is one wave's job and costs its groups plus about two groups' worth of
 // per-lane shifts and the wave's reduction; whole groups of padding cost
 // nothing.  The resident waves (16 per CU) take about

@@ -2,10 +2,10 @@
 
 The CRC32C kernels give each stripe of a record to one wave: the stripe is
 ``groups`` groups of 1 KiB, lane l folds the 16-byte word at l * 16 of every
-group as one slicing-by-4 chain of 4 dwords, and the lane keeps 8 chains,
-chain c taking the stripe's groups c, c + 8, ... (counted from its first
-group of record bytes), each advanced by shift(s, 8 * 1024 - 16) before its
-next word.  At the end the chains are combined by Horner's rule in the order
+group, and the lane keeps 6 chains, chain c taking the stripe's groups c,
+c + 6, ... (counted from its first group of record bytes):
+acc' = shift(acc, 6 * 1024) ^ R(word), R the word's raw CRC from a zero
+register in four slicing-by-4 steps.  At the end the chains are combined by Horner's rule in the order
 of their last groups (shift(s, 1024) between them), each lane's register is
 shifted past the lanes after it (x^(8 * 16 * (63 - l))), and the wave's XOR
 is the stripe's raw CRC.  The first stripe is padded in front with zero bytes
@@ -14,11 +14,16 @@ the stripes after it with the powers x^(8 * stripe_bytes * 2^i) (in the
 workgroup, or by the combine kernel) and the initial value's term is added.
 
 This replays that scheme in Python with the kernel's own tables (slicing,
-advance, chain and lane shifts), over the stripe plans the library picks, and
-checks every record's CRC32C against the oracle's (the reference's
+advance by nibbles, chain and lane shifts), over the stripe plans the library
+picks, and checks every record's CRC32C against the oracle's (the reference's
 kvsnap_crc32c_extend, csrc/dataplane/io.cpp:39-44); a variant that combines
-the chains in the wrong order must fail.
+the chains in the wrong order must fail.  It also replays the kernel's LDS
+addressing (v_perm_b32 byte moves into a per-lane column constant): every
+lane's lookups of the private slicing and advance tables land in its own
+bank and on the entry the fill put there.
 """
+import functools
+import operator
 import random
 
 import pytest
@@ -26,7 +31,7 @@ import pytest
 import oracle
 from tests.test_checked_crc_math import gf_mul, xpow8n
 
-RUN, CHAINS, LANES = 16, 8, 64
+RUN, CHAINS, LANES = 16, 6, 64
 GROUP = LANES * RUN
 MAX_STRIPES, RESIDENT_WAVES = 64, 256 * 16
 
@@ -36,8 +41,8 @@ def slicing_tables():
 
 
 S = slicing_tables()
-ADVANCE = xpow8n(CHAINS * GROUP - RUN)
-G = [[gf_mul(ADVANCE, v << (8 * k)) for v in range(256)] for k in range(4)]
+ADVANCE = xpow8n(CHAINS * GROUP)
+GN = [[gf_mul(ADVANCE, v << (4 * i)) for v in range(16)] for i in range(8)]     # the advance, by nibbles
 BEHIND = xpow8n(GROUP)
 H = [[gf_mul(BEHIND, v << (8 * k)) for v in range(256)] for k in range(4)]
 M = [xpow8n(RUN * (63 - lane)) for lane in range(LANES)]
@@ -45,6 +50,10 @@ M = [xpow8n(RUN * (63 - lane)) for lane in range(LANES)]
 
 def lookup(tables, x):
     return tables[0][x & 0xFF] ^ tables[1][(x >> 8) & 0xFF] ^ tables[2][(x >> 16) & 0xFF] ^ tables[3][x >> 24]
+
+
+def advance(x):
+    return functools.reduce(operator.xor, (GN[i][(x >> (4 * i)) & 15] for i in range(8)))
 
 
 def chain(state, run):
@@ -86,7 +95,7 @@ def stripe_raw(record, start, groups, wrong_order=False):
         acc = [0] * CHAINS
         for g in range(lead, groups):
             c = (g - lead) % CHAINS
-            acc[c] = chain(lookup(G, acc[c]), run(g, lane))
+            acc[c] = advance(acc[c]) ^ chain(0, run(g, lane))
         x = 0
         order = range(CHAINS - 1, -1, -1) if not wrong_order else range(CHAINS)
         for i, d in enumerate(order):
@@ -150,3 +159,67 @@ def test_a_scheme_that_combines_the_chains_in_the_wrong_order_fails():
     groups, stripes, pad = 11, 1, 0
     assert record_crc(record, groups, stripes, pad) == oracle.crc32c(record)
     assert record_crc(record, groups, stripes, pad, wrong_order=True) != oracle.crc32c(record)
+
+
+# ---- the LDS layout of the private tables ------------------------------------------------------------
+
+H_BYTES, GN_BYTES, S_BYTES = 4096, 16384, 131072
+GN_AT, S_AT = H_BYTES, H_BYTES + GN_BYTES
+
+
+def perm(x, cols, selector):
+    """v_perm_b32(x, cols, selector): byte k of the result is byte (selector byte k) of {x: 7-4, cols: 3-0};
+    selector 0x0C gives 0x00."""
+    pool = cols.to_bytes(4, "little") + x.to_bytes(4, "little")
+    out = 0
+    for k in range(4):
+        sel = (selector >> (8 * k)) & 0xFF
+        out |= (0 if sel == 0x0C else pool[sel]) << (8 * k)
+    return out
+
+
+def columns(lane):
+    col = (lane & 31) * 4
+    return col | ((col + 128) << 8) | (1 << 16)
+
+
+S_SELECTORS = (0x0C0C0400, 0x0C0C0501, 0x0C020600, 0x0C020701)
+GN_LOOKUPS = [(page, half, 0x0C0C0000 | ((4 + page) << 8) | half) for page in range(4) for half in (0, 1)]
+
+
+def filled_lds():
+    """The bytes crc_fill_tables writes: {byte address: table word}."""
+    lds = {}
+    for t in range(1024):                               # S entry t, its 32 lane columns
+        table, v = t >> 8, t & 255
+        for k in range(32):
+            lds[S_AT + (table >> 1) * 65536 + v * 256 + (table & 1) * 128 + 4 * k] = S[table][v]
+        e = t >> 3                                      # Gn entry e, four lane columns
+        nib_table, nib = e >> 4, e & 15
+        for k in range(4):
+            lds[GN_AT + (nib_table >> 1) * 4096 + nib * 256 + (nib_table & 1) * 128 + (t & 7) * 16 + 4 * k] = \
+                GN[nib_table][nib]
+        lds[4 * t] = H[t >> 8][t & 255]
+    return lds
+
+
+def test_the_private_tables_fill_the_lds_once_and_every_lane_reads_its_own_bank_and_entry():
+    lds = filled_lds()
+    assert len(lds) == (H_BYTES + GN_BYTES + S_BYTES) // 4 and max(lds) < H_BYTES + GN_BYTES + S_BYTES
+    rng = random.Random(5)
+    for lane in range(64):
+        cols = columns(lane)
+        for x in [0, 0xFFFFFFFF] + [rng.getrandbits(32) for _ in range(40)]:
+            for i, selector in enumerate(S_SELECTORS):          # slicing-by-4 lookups, crc_step_all
+                address = S_AT + perm(x, cols, selector)
+                assert (address // 4) % 32 == lane % 32
+                assert lds[address] == S[i][(x >> (8 * i)) & 0xFF]
+            lo, hi = x & 0x0F0F0F0F, (x >> 4) & 0x0F0F0F0F       # the advance, crc_fold_batch
+            found = 0
+            for page, half, selector in GN_LOOKUPS:
+                address = GN_AT + page * 4096 + perm(hi if half else lo, cols, selector)
+                assert (address // 4) % 32 == lane % 32
+                nibble = 2 * page + half
+                assert lds[address] == GN[nibble][(x >> (4 * nibble)) & 15]
+                found ^= lds[address]
+            assert found == gf_mul(ADVANCE, x)
