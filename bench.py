@@ -304,7 +304,10 @@ def run_save_restore(args):
     layers, num_blocks, block_size, tokens = 36, 16384, 16, 8192
     session = tokens // block_size
     caches, backing = synth.make_caches(layers, num_blocks, block_size=block_size, layout=args.layout)
-    plane = TorchBlockDataPlane(caches, block_size, session * layers * 65536 + (64 << 20))
+    # Nothing else runs on the GPU here, so the restore kernel reads the pinned records in place (about 3 %
+    # faster than the copy engines, the library's default for serving beside a decode).
+    plane = TorchBlockDataPlane(caches, block_size, session * layers * 65536 + (64 << 20),
+                                restore_mode=args.restore_mode or "kernel")
     plane.warm_up()
     keep = synth.fill(plane, 0)
     torch.cuda.synchronize()
@@ -461,7 +464,7 @@ def run_save_restore(args):
         "config": {"workload": "qwen3-8b-8k-token-snapshot-save-then-restore", "layers": layers, "kv_heads": 8,
                    "head_dim": 128, "block_size": block_size, "cache_blocks": num_blocks, "session_blocks": session,
                    "snapshot_bytes": total, "kv_dtype": "bf16", "layout": args.layout,
-                   "parallelism": "none (one GPU)"},
+                   "restore_mode": plane.restore_mode, "parallelism": "none (one GPU)"},
         "hash_depth": args.hash_depth,
         "save_ms": round(lat["save"], 3),
         "save_gbps": round(total / lat["save"] / 1e6, 2),
@@ -1316,7 +1319,7 @@ def main():
     parser.add_argument("--no-digests", action="store_true",
                         help="duplex: saves without GPU CRC32C / SHA-256 (the link alone)")
     parser.add_argument("--restore-mode", choices=("kernel", "dma"), default=None,
-                        help="duplex, rotating-fp8: how restores cross the link")
+                        help="save-restore, duplex, rotating-fp8: how restores cross the link")
     parser.add_argument("--disk-dir", default=None, help="disk-fork, turns, ttft: where the blob files go")
     parser.add_argument("--cpu-seconds", type=float, default=0.6,
                         help="save-restore: seconds per leg and thread count of the CPU baseline")

@@ -1203,7 +1203,9 @@ __device__ __forceinline__ void sha_rounds_pair(uint32_t x[4], const u32x4 (*slo
     x[0] += x0; x[1] += x1; x[2] += x2; x[3] += x3;
 }
 
-constexpr int kShaThreads = 192;  // waves 0-1: rounds (32 records each); wave 2: message schedule (64 records)
+constexpr int kShaRoundWaves = 2;                  // round waves per workgroup, 32 records each
+constexpr int kShaRecords = 32 * kShaRoundWaves;   // records per workgroup
+constexpr int kShaThreads = 64 * (kShaRoundWaves + 1);  // the round waves, then the message-schedule wave
 constexpr int kShaStep = 4;  // blocks per barrier; the producer fills one half while the rounds read the other
 
 // The producer's step for block `blk`: expand the words loaded for it, then
@@ -1233,14 +1235,14 @@ __global__ __launch_bounds__(kShaThreads) void sha256_kernel(const uint8_t* __re
                                                              uint32_t* __restrict__ state,
                                                              uint32_t* __restrict__ out) {
     __shared__ u32x4 sched[2][kShaStep][kShaBlockQuads][kShaColumns];
-    const bool producer = threadIdx.x >= 128;
+    const bool producer = threadIdx.x >= 64 * kShaRoundWaves;
     const int lane = threadIdx.x & 63;
     const int bank = (lane >> 2) & 3;
     const bool a_lane = bank & 1;
-    // Record of this lane within the workgroup's 64.
+    // Record of this lane within the workgroup's kShaRecords (producer lanes past them idle).
     const int rec = producer ? lane : (threadIdx.x >> 6) * 32 + (lane >> 4) * 8 + (bank >> 1) * 4 + (lane & 3);
-    const int64_t r = static_cast<int64_t>(blockIdx.x) * 64 + rec;
-    const bool live = r < n_records;
+    const int64_t r = static_cast<int64_t>(blockIdx.x) * kShaRecords + rec;
+    const bool live = rec < kShaRecords && r < n_records;
     // Lanes past the last record hash record 0 (in bounds) and store nothing.
     const uint8_t* p = records + (live ? r : 0) * pitch;
     const uint64_t whole = record_bytes / 64;
@@ -1763,7 +1765,7 @@ int kvsnap_sha256_records_range(const void* records, uint64_t record_bytes, uint
             throw std::runtime_error("SHA-256 output and state must be 16-byte aligned");
         hipStream_t s = reinterpret_cast<hipStream_t>(stream);
         const bool aligned = (reinterpret_cast<uintptr_t>(records) % 16 == 0) && (record_pitch % 16 == 0);
-        const unsigned grid = static_cast<unsigned>((n_records + 63) / 64);
+        const unsigned grid = static_cast<unsigned>((n_records + kShaRecords - 1) / kShaRecords);
         const auto* base = static_cast<const uint8_t*>(records);
         auto* words = reinterpret_cast<uint32_t*>(out);
         if (aligned)
