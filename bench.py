@@ -523,6 +523,14 @@ def run_save_restore(args):
             "metric", "value", "unit", "copy_alone_gbps", "rounds", "record_bytes", "sessions_tokens",
             "decode_step_ms", "p99_compute_stall_ms", "save_mode", "restore_mode", "restore_programs",
             "byte_exact", "saves_hashed", "digests_exact", "streams")}
+    if not args.no_duplex:
+        # The same session's saves and restores overlapped from two threads, as a connector's save threads
+        # and loader thread issue them (every save still hashed): the link's two directions at once.
+        duplex = run_duplex(args)
+        out["duplex"] = {key: duplex[key] for key in (
+            "metric", "value", "unit", "steps", "ms_per_step", "duplex_link_gbps", "restore_mode", "save_mode",
+            "restore_stream_check", "parity", "streams")}
+    out["hw_queues"] = os.environ.get("GPU_MAX_HW_QUEUES")
     return out
 
 
@@ -852,6 +860,7 @@ def run_duplex(args):
     del up_src, down_dst, dev_a, dev_b
     log(f"both directions at once: {max(duplex):.1f} GB/s aggregate")
 
+    streams = plane.stream_report()
     for b in buffers:
         b.close()
     plane.close()
@@ -859,7 +868,7 @@ def run_duplex(args):
             "value": round(2 * total / (ms_per_step * 1e6), 3), "unit": "GB/s", "steps": args.steps,
             "warmup": args.warmup, "ms_per_step": round(ms_per_step, 3), "snapshot_bytes": total,
             "duplex_link_gbps": round(max(duplex), 2), "layout": args.layout, "restore_mode": plane.restore_mode,
-            "save_mode": plane.save_mode, "restore_stream_check": plane.restore_stream_check,
+            "save_mode": plane.save_mode, "restore_stream_check": plane.restore_stream_check, "streams": streams,
             "parity": {"restore_byte_exact": exact, "digests_bit_exact": digests_exact},
             "note": "session k restored while session k + 1 is saved (two host threads, two pinned buffers); "
                     "each step still saves 1.208 GB with CRC32C + SHA-256 and restores 1.208 GB"}
@@ -1326,11 +1335,19 @@ def main():
     parser.add_argument("--no-cpu-baseline", action="store_true")
     parser.add_argument("--no-rotating", action="store_true",
                         help="save-restore: leave out the rotating fp8 sessions beside a decode")
+    parser.add_argument("--no-duplex", action="store_true",
+                        help="save-restore: leave out the saves and restores overlapped from two threads")
     args = parser.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: every GPU saves and restores its own KV shard over its own host link, "
               "so there is no multi-GPU step to time here (run with --gpus 1)", file=sys.stderr)
         sys.exit(2)
+    # A plane runs the engine's stream, its copy stream, a restore stream and hash streams side by side, and
+    # streams only run side by side on hardware queues of their own: HIP's default of four is too few for a
+    # restore stream and two hash streams beside the copy stream (overlapped saves and restores then wait on
+    # one another's queues).  At least eight, set before HIP starts.
+    if int(os.environ.get("GPU_MAX_HW_QUEUES") or 4) < 8:
+        os.environ["GPU_MAX_HW_QUEUES"] = "8"
     import torch
     torch.cuda.set_device(0)
     runner = {"save-restore": run_save_restore, "disk-fork": run_disk_fork, "rotating-fp8": run_rotating,
