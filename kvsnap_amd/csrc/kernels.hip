@@ -1153,11 +1153,6 @@ __device__ __forceinline__ uint32_t rotr_v(uint32_t x, uint32_t n) { return __bu
 // from here on (no constant folding of lane masks, no reassociating sums).
 __device__ __forceinline__ void opaque(uint32_t& x) { asm("" : "+v"(x)); }
 
-__device__ __forceinline__ uint32_t sha_word(const u32x4 (*slot)[kShaColumns], int column, int t) {
-    const u32x4 q = slot[t >> 2][column];
-    return (t & 3) == 0 ? q.x : (t & 3) == 1 ? q.y : (t & 3) == 2 ? q.z : q.w;
-}
-
 __device__ __forceinline__ uint32_t from_a_partner(uint32_t x) {
     return static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(x), kDppRowShl4, 0xF, kEBanks, false));
 }
@@ -1169,18 +1164,31 @@ __device__ __forceinline__ uint32_t from_e_partner(uint32_t x) {
 // The 64 rounds of one block.  W is computed one round ahead and its first
 // term two rounds ahead, so the two instructions between V and the round's
 // DPP add are independent work (a DPP read waits two instructions after the
-// write of any register it reads).
+// write of any register it reads).  The W+K words come from LDS four rounds
+// to a 16-byte read, each read issued kShaAhead quads (4 rounds a quad)
+// before its first use, so its latency hides behind the rounds before it.
+constexpr int kShaAhead = 2;
+
+__device__ __forceinline__ uint32_t quad_word(const u32x4& q, int t) {
+    return (t & 3) == 0 ? q.x : (t & 3) == 1 ? q.y : (t & 3) == 2 ? q.z : q.w;
+}
+
 __device__ __forceinline__ void sha_rounds_pair(uint32_t x[4], const u32x4 (*slot)[kShaColumns], int column,
                                                 const ShaHalf& k) {
+    u32x4 q[kShaBlockQuads];
+#pragma unroll
+    for (int j = 0; j <= kShaAhead; ++j) q[j] = slot[j][column];
     uint32_t x0 = x[0], x1 = x[1], x2 = x[2], x3 = x[3];
-    uint32_t z_next = (x2 ^ k.m) + sha_word(slot, column, 1);  // round 1's X3 is X2 now
+    uint32_t z_next = (x2 ^ k.m) + quad_word(q[0], 1);  // round 1's X3 is X2 now
     opaque(z_next);
-    uint32_t z = (x3 ^ k.m) + sha_word(slot, column, 0);
+    uint32_t z = (x3 ^ k.m) + quad_word(q[0], 0);
     opaque(z);
     uint32_t w = from_a_partner(x3) + z;
     opaque(w);
 #pragma unroll
     for (int t = 0; t < 64; ++t) {
+        if ((t & 3) == 0 && (t >> 2) + kShaAhead + 1 < kShaBlockQuads)
+            q[(t >> 2) + kShaAhead + 1] = slot[(t >> 2) + kShaAhead + 1][column];
         const uint32_t s = xor3(rotr_v(x0, k.r1), rotr_v(x0, k.r2), rotr_v(x0, k.r3));
         // bitop3 tables index bits as (src0 << 2) | (src1 << 1) | src2.
         const uint32_t u = __builtin_amdgcn_bitop3_b32(x0, x1, k.m, 0xD2);  // m ? ~(x0 ^ x1) : x0
@@ -1189,7 +1197,7 @@ __device__ __forceinline__ void sha_rounds_pair(uint32_t x[4], const u32x4 (*slo
         opaque(v);
         uint32_t z_after = 0;
         if (t + 2 < 64) {
-            z_after = (x1 ^ k.m) + sha_word(slot, column, t + 2);  // h + W+K | -d of round t + 2
+            z_after = (x1 ^ k.m) + quad_word(q[(t + 2) >> 2], t + 2);  // h + W+K | -d of round t + 2
             opaque(z_after);
         }
         if (t + 1 < 64) {
