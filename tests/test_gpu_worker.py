@@ -131,3 +131,62 @@ def test_a_session_saved_and_loaded_through_the_worker_is_what_the_next_forward_
         worker.shutdown()
         torch.cuda.synchronize()
         plane.close()
+
+
+@pytest.mark.parametrize("restore_mode", ["kernel", "dma"])
+def test_a_worker_that_registers_vllm_s_caches_saves_and_loads_what_the_oracle_says(hip_library, oracle_lib,
+                                                                                   restore_mode):
+    """register_kv_caches (reference vllm.py:226-240): the worker builds and warms the plane and its host
+    tier, publishes the layout every snapshot then records, and a turn saved and loaded through the hooks
+    leaves the cache equal to the oracle's scatter of the oracle's records."""
+    from kvsnap_amd.layout import describe_layer, layout_identity
+    caches, backing = synth.make_caches(LAYERS, BLOCKS, layout="vllm")
+    worker = KvsnapWorker(host_tier_bytes=64 << 20, block_size=BLOCK_SIZE, capacity_bytes=160 << 20,
+                          plane_options={"restore_mode": restore_mode}, verify="gpu")
+    try:
+        layout = worker.register_kv_caches(caches)
+        plane = worker.dataplane
+        assert plane.restore_mode == restore_mode and worker.host_tier is not None
+        assert layout == layout_identity([describe_layer(n, caches[n], BLOCK_SIZE) for n in sorted(caches)])
+        keep = synth.fill(plane, 6)
+        torch.cuda.synchronize()
+        del keep
+        rng = random.Random(12)
+        source = rng.sample(range(1, BLOCKS), 24)
+        target = rng.sample([b for b in range(1, BLOCKS) if b not in source], 24)
+        tokens = 24 * BLOCK_SIZE - 9
+        size = plane.block_bytes
+        host = backing.view(torch.uint8).cpu().numpy().reshape(-1).copy()
+        base = backing.data_ptr()
+        host_spans = [(host.ctypes.data + (s[1] - base), s[2], s[0], s[3]) for s in plane.spans()]
+        records = oracle_lib.gather(host_spans, source, size)
+        oracle_lib.zero_tail(records[-1], plane.layers, tokens % BLOCK_SIZE)
+
+        worker.bind_connector_metadata(KvsnapMetadata(saves=[Transfer("s", source, num_kv_tokens=tokens)]))
+        worker.wait_for_save()
+        worker.clear_connector_metadata()
+        run_until(worker, lambda sending, receiving: "s" in sending, finished={"s"})
+        run_until(worker, lambda sending, receiving: not worker._saves)
+        snapshot = worker.build_connector_worker_meta().prepared["s"]
+        assert snapshot["kv_layout"] == layout
+        crcs, shas = oracle_lib.digest_records(records.ctypes.data, size, size, len(source), threads=4)
+        assert [(s["blob_id"], s["crc32c"]) for s in snapshot["segments"]] == \
+            [(bytes(h).hex(), int(c)) for h, c in zip(shas, crcs)]
+
+        worker.bind_connector_metadata(KvsnapMetadata(loads=[Transfer("l", target, snapshot=snapshot)]))
+        worker.start_load_kv(None)
+        worker.clear_connector_metadata()
+        run_until(worker, lambda sending, receiving: "l" in receiving)
+        run_until(worker, lambda sending, receiving: not worker._loads)
+        torch.cuda.synchronize()
+        report = worker.build_connector_worker_meta()
+        assert report.loaded == ["l"] and report.failed_loads == []
+        oracle_lib.scatter(host_spans, target, [records.ctypes.data + i * size for i in range(len(target))])
+        after = backing.view(torch.uint8).cpu().numpy().reshape(-1)
+        changed = np.flatnonzero(after != host)
+        assert changed.size == 0, f"{changed.size} bytes differ from the oracle's scatter, first at {changed[0]}"
+    finally:
+        worker.shutdown()
+        torch.cuda.synchronize()
+        if worker.dataplane is not None:
+            worker.dataplane.close()
