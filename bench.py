@@ -1343,12 +1343,6 @@ def main():
         print("bench.py measures one GPU: every GPU saves and restores its own KV shard over its own host link, "
               "so there is no multi-GPU step to time here (run with --gpus 1)", file=sys.stderr)
         sys.exit(2)
-    # A plane runs the engine's stream, its copy stream, a restore stream and hash streams side by side, and
-    # streams only run side by side on hardware queues of their own: HIP's default of four is too few for a
-    # restore stream and two hash streams beside the copy stream (overlapped saves and restores then wait on
-    # one another's queues).  At least eight, set before HIP starts.
-    if int(os.environ.get("GPU_MAX_HW_QUEUES") or 4) < 8:
-        os.environ["GPU_MAX_HW_QUEUES"] = "8"
     import torch
     torch.cuda.set_device(0)
     runner = {"save-restore": run_save_restore, "disk-fork": run_disk_fork, "rotating-fp8": run_rotating,

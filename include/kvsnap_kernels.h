@@ -161,6 +161,17 @@ int kvsnap_sha256_records_range(const void* records, uint64_t record_bytes, uint
                                 int64_t n_records, uint64_t first_block, uint64_t end_block, uint32_t* state,
                                 uint8_t* out, uintptr_t stream);
 
+/* Up to 8 independent kvsnap_sha256_records_range calls in one launch (no
+ * reference counterpart: the reference hashes each save's blocks on host
+ * threads).  Range i is the i-th entry of every host array: records address,
+ * record bytes and pitch, record count, first and end block, state and out
+ * addresses, each checked as kvsnap_sha256_records_range checks them.  Saves
+ * hashing at the same time share each launch, so they hash side by side on
+ * one stream instead of in turn. */
+int kvsnap_sha256_ranges(int count, const uint64_t* records, const uint64_t* record_bytes,
+                         const uint64_t* record_pitches, const int64_t* n_records, const uint64_t* first_blocks,
+                         const uint64_t* end_blocks, const uint64_t* states, const uint64_t* outs, uintptr_t stream);
+
 /* Streams of the data plane's own (no reference counterpart; the reference
  * copies on one stream).  kvsnap_stream_create makes a non-blocking stream of
  * default priority on `device`; kvsnap_stream_destroy waits for its work and

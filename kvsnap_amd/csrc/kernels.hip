@@ -1230,26 +1230,26 @@ __device__ __forceinline__ void sha_produce(const uint8_t* __restrict__ p, uint6
     sha_schedule(w, slot, lane);
 }
 
-// Blocks [b0, b1) of every record's chain.  b0 = 0 starts from the FIPS
-// 180-4 initial value, otherwise from `state` (8 words per record, as a
-// previous launch left them); b1 = nblocks writes the digest to `out`,
-// otherwise the chaining state back to `state`.  A whole hash in one launch
-// holds its stream (and any stream sharing its hardware queue) for the whole
-// chain; the host can run it as a series of shorter launches instead.
+using ShaSchedule = u32x4[2][kShaStep][kShaBlockQuads][kShaColumns];
+
+// Blocks [b0, b1) of the chains of the `group`-th kShaRecords records.  b0 =
+// 0 starts from the FIPS 180-4 initial value, otherwise from `state` (8 words
+// per record, as a previous launch left them); b1 = nblocks writes the digest
+// to `out`, otherwise the chaining state back to `state`.  A whole hash in
+// one launch holds its stream (and any stream sharing its hardware queue) for
+// the whole chain; the host can run it as a series of shorter launches.
 template <bool kAligned>
-__global__ __launch_bounds__(kShaThreads) void sha256_kernel(const uint8_t* __restrict__ records,
-                                                             uint64_t record_bytes, uint64_t pitch,
-                                                             int64_t n_records, uint64_t b0, uint64_t b1,
-                                                             uint32_t* __restrict__ state,
-                                                             uint32_t* __restrict__ out) {
-    __shared__ u32x4 sched[2][kShaStep][kShaBlockQuads][kShaColumns];
+__device__ __forceinline__ void sha256_group(ShaSchedule& sched, const uint8_t* __restrict__ records,
+                                             uint64_t record_bytes, uint64_t pitch, int64_t n_records, uint64_t b0,
+                                             uint64_t b1, uint32_t* __restrict__ state, uint32_t* __restrict__ out,
+                                             int64_t group) {
     const bool producer = threadIdx.x >= 64 * kShaRoundWaves;
     const int lane = threadIdx.x & 63;
     const int bank = (lane >> 2) & 3;
     const bool a_lane = bank & 1;
     // Record of this lane within the workgroup's kShaRecords (producer lanes past them idle).
     const int rec = producer ? lane : (threadIdx.x >> 6) * 32 + (lane >> 4) * 8 + (bank >> 1) * 4 + (lane & 3);
-    const int64_t r = static_cast<int64_t>(blockIdx.x) * kShaRecords + rec;
+    const int64_t r = group * kShaRecords + rec;
     const bool live = rec < kShaRecords && r < n_records;
     // Lanes past the last record hash record 0 (in bounds) and store nothing.
     const uint8_t* p = records + (live ? r : 0) * pitch;
@@ -1308,6 +1308,44 @@ __global__ __launch_bounds__(kShaThreads) void sha256_kernel(const uint8_t* __re
         else
             *reinterpret_cast<u32x4*>(chain) = u32x4{x[0], x[1], x[2], x[3]};
     }
+}
+
+template <bool kAligned>
+__global__ __launch_bounds__(kShaThreads) void sha256_kernel(const uint8_t* __restrict__ records,
+                                                             uint64_t record_bytes, uint64_t pitch,
+                                                             int64_t n_records, uint64_t b0, uint64_t b1,
+                                                             uint32_t* __restrict__ state,
+                                                             uint32_t* __restrict__ out) {
+    __shared__ ShaSchedule sched;
+    sha256_group<kAligned>(sched, records, record_bytes, pitch, n_records, b0, b1, state, out, blockIdx.x);
+}
+
+// Several independent ranges in one launch: range blockIdx.y, its blockIdx.x-th
+// group of records.  Saves hashing at the same time share each launch, so
+// they hash side by side on one stream (and one hardware queue) instead of in
+// turn.
+constexpr int kShaMaxRanges = 8;
+
+struct ShaRange {
+    const uint8_t* records;
+    uint64_t record_bytes, pitch;
+    int64_t n_records;
+    uint64_t b0, b1;
+    uint32_t* state;
+    uint32_t* out;
+};
+
+struct ShaRanges {
+    ShaRange r[kShaMaxRanges];
+};
+
+template <bool kAligned>
+__global__ __launch_bounds__(kShaThreads) void sha256_ranges_kernel(ShaRanges ranges) {
+    __shared__ ShaSchedule sched;
+    const ShaRange& g = ranges.r[blockIdx.y];
+    if (static_cast<int64_t>(blockIdx.x) * kShaRecords >= g.n_records) return;  // the whole workgroup
+    sha256_group<kAligned>(sched, g.records, g.record_bytes, g.pitch, g.n_records, g.b0, g.b1, g.state, g.out,
+                           blockIdx.x);
 }
 
 // ----------------------------------------------------------------- host helpers
@@ -1757,20 +1795,70 @@ uint64_t kvsnap_sha256_blocks(uint64_t record_bytes) {
     return whole + (record_bytes - 64 * whole + 9 <= 64 ? 1 : 2);
 }
 
+}  // extern "C"
+
+namespace {
+
+// The checks every SHA-256 range passes before a launch.
+void check_sha_range(const void* records, uint64_t record_bytes, int64_t n_records, uint64_t first_block,
+                     uint64_t end_block, const uint32_t* state, const uint8_t* out) {
+    if (n_records < 0) throw std::runtime_error("negative record count");
+    const uint64_t nblocks = kvsnap_sha256_blocks(record_bytes);
+    if (first_block >= end_block || end_block > nblocks) throw std::runtime_error("SHA-256 block range out of order");
+    if (!records && record_bytes) throw std::runtime_error("SHA-256 needs device pointers");
+    if (end_block == nblocks && !out) throw std::runtime_error("SHA-256 needs an output for the last blocks");
+    if ((first_block > 0 || end_block < nblocks) && !state)
+        throw std::runtime_error("SHA-256 over part of the chain needs a state buffer");
+    if (reinterpret_cast<uintptr_t>(out) % 16 || reinterpret_cast<uintptr_t>(state) % 16)
+        throw std::runtime_error("SHA-256 output and state must be 16-byte aligned");
+}
+
+}  // namespace
+
+extern "C" {
+
+int kvsnap_sha256_ranges(int count, const uint64_t* records, const uint64_t* record_bytes,
+                         const uint64_t* record_pitches, const int64_t* n_records, const uint64_t* first_blocks,
+                         const uint64_t* end_blocks, const uint64_t* states, const uint64_t* outs, uintptr_t stream) {
+    return guard([&] {
+        if (count < 0 || count > kShaMaxRanges) throw std::runtime_error("SHA-256: 0 to 8 ranges per launch");
+        if (count && (!records || !record_bytes || !record_pitches || !n_records || !first_blocks || !end_blocks ||
+                      !states || !outs))
+            throw std::runtime_error("SHA-256 ranges need every table");
+        ShaRanges ranges{};
+        int used = 0;
+        int64_t groups = 0;
+        bool aligned = true;
+        for (int i = 0; i < count; ++i) {
+            const auto* base = reinterpret_cast<const uint8_t*>(records[i]);
+            auto* state = reinterpret_cast<uint32_t*>(states[i]);
+            auto* out = reinterpret_cast<uint8_t*>(outs[i]);
+            check_sha_range(base, record_bytes[i], n_records[i], first_blocks[i], end_blocks[i], state, out);
+            if (n_records[i] == 0) continue;
+            aligned = aligned && records[i] % 16 == 0 && record_pitches[i] % 16 == 0;
+            ranges.r[used++] = ShaRange{base, record_bytes[i], record_pitches[i], n_records[i], first_blocks[i],
+                                        end_blocks[i], state, reinterpret_cast<uint32_t*>(out)};
+            groups = std::max<int64_t>(groups, (n_records[i] + kShaRecords - 1) / kShaRecords);
+        }
+        if (!used) return;
+        if (groups > (int64_t(1) << 30)) throw std::runtime_error("SHA-256: too many records");
+        hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+        const dim3 grid(static_cast<unsigned>(groups), static_cast<unsigned>(used));
+        if (aligned)
+            hipLaunchKernelGGL(sha256_ranges_kernel<true>, grid, dim3(kShaThreads), 0, s, ranges);
+        else
+            hipLaunchKernelGGL(sha256_ranges_kernel<false>, grid, dim3(kShaThreads), 0, s, ranges);
+        check_launch("sha256 ranges");
+    });
+}
+
 int kvsnap_sha256_records_range(const void* records, uint64_t record_bytes, uint64_t record_pitch,
                                 int64_t n_records, uint64_t first_block, uint64_t end_block, uint32_t* state,
                                 uint8_t* out, uintptr_t stream) {
     return guard([&] {
         if (n_records < 0) throw std::runtime_error("negative record count");
         if (n_records == 0) return;
-        const uint64_t nblocks = kvsnap_sha256_blocks(record_bytes);
-        if (first_block >= end_block || end_block > nblocks) throw std::runtime_error("SHA-256 block range out of order");
-        if (!records && record_bytes) throw std::runtime_error("SHA-256 needs device pointers");
-        if (end_block == nblocks && !out) throw std::runtime_error("SHA-256 needs an output for the last blocks");
-        if ((first_block > 0 || end_block < nblocks) && !state)
-            throw std::runtime_error("SHA-256 over part of the chain needs a state buffer");
-        if (reinterpret_cast<uintptr_t>(out) % 16 || reinterpret_cast<uintptr_t>(state) % 16)
-            throw std::runtime_error("SHA-256 output and state must be 16-byte aligned");
+        check_sha_range(records, record_bytes, n_records, first_block, end_block, state, out);
         hipStream_t s = reinterpret_cast<hipStream_t>(stream);
         const bool aligned = (reinterpret_cast<uintptr_t>(records) % 16 == 0) && (record_pitch % 16 == 0);
         const unsigned grid = static_cast<unsigned>((n_records + kShaRecords - 1) / kShaRecords);
