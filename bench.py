@@ -65,16 +65,16 @@ LATENCY_SAMPLES = 20
 # MI355X's host link, PCIe 5.0 x16: 32 GT/s x 16 lanes, 128b/130b encoding, per direction.
 PCIE5_X16_GBPS = round(32 * 16 * 128 / 130 / 8, 2)
 # SHA-256 runs one dependency chain per record (two lanes of a round wave).
-# The round wave issues 648 VALU per 64-byte block (counted in the gfx950 ISA
-# of sha256_kernel: 192 alignbit, 192 bitop3, 127 DPP adds, 65 add3, 64 xad,
-# 8 others); a wave64 VALU takes 4 cycles of its SIMD at the 2.4 GHz peak
-# engine clock.  All chains run side by side (one round wave per 32 records).
-# Timed alone on one wave, the round's own instruction sequence takes 49.6
-# cycles (its two lane-moving DPP adds cost about four cycles each beyond
-# their issue slots): the bound at that rate is reported beside the nominal one.
-SHA_VALU_PER_BLOCK = 648
+# The round wave issues 596 VALU per 64-byte block (counted in the gfx950 ISA
+# of sha256_kernel: 192 alignbit, 192 bitop3, 74 DPP adds, 64 add3, 64 xad,
+# 10 others); a wave64 VALU takes 4 cycles of its SIMD at the 2.4 GHz peak
+# engine clock (the kernel's own clock counters read 2.39-2.40 GHz).  All
+# chains run side by side (one round wave per 32 records).  Timed alone on
+# one wave, a round's own 9-VALU sequence takes 37.5 cycles: the bound at that
+# rate is reported beside the nominal one.
+SHA_VALU_PER_BLOCK = 596
 SHA_CYCLES_PER_VALU = 4
-SHA_ROUND_CYCLES = 49.6
+SHA_ROUND_CYCLES = 37.5
 ENGINE_CLOCK_GHZ = 2.4
 
 

@@ -1000,17 +1000,17 @@ __global__ __launch_bounds__(64) void restore_checked_finish_kernel(
 //
 // SHA-256 is a sequential chain of 64-byte compressions within a record, so
 // records are the only parallelism, and a few hundred records fill only a few
-// dozen of the chip's 1024 SIMDs.  A record's time is therefore the issue time
-// of its chain (a wave64 VALU instruction takes 4 cycles of its SIMD), and
-// everything that does not depend on the chaining state is moved off it:
-//   * a producer wave (one record per lane) loads each block a step ahead,
-//     byte-swaps it, expands the message schedule and adds the round
-//     constants (W[t] + K[t]) into LDS;
+// dozen of the chip's 1024 SIMDs.  A record's time is therefore the time of
+// its chain of rounds (a wave64 VALU instruction takes 4 cycles of its SIMD),
+// and everything that does not depend on the chaining state is moved off it:
+//   * two producer waves (one record per lane, alternate blocks of a step)
+//     load each block a step ahead, byte-swap it, expand the message schedule
+//     and add the round constants (W[t] + K[t]) into LDS;
 //   * two round waves run only the 64 rounds, two lanes per record (the
-//     e-half and the a-half of each round side by side; see sha_rounds_pair),
-//     10 VALU per round.
-// Workgroup = two round waves + one producer wave over the same 64 records;
-// the producer fills one half of a double buffer of kShaStep blocks while the
+//     e-half and the a-half of each round side by side, the a-half one round
+//     behind; see sha_block), 10 VALU per round.
+// Workgroup = two round waves + two producer waves over the same 64 records;
+// the producers fill one half of a double buffer of kShaStep blocks while the
 // round waves read the other.
 
 __constant__ uint32_t kSha[64] = {
@@ -1125,23 +1125,27 @@ __device__ __forceinline__ void sha_schedule(uint32_t w[16], u32x4 (*slot)[kShaC
     }
 }
 
-// Round waves: two lanes per record.  Within each 16-lane row, banks 0 and 2
-// (lanes 0-3, 8-11) are "e-lanes" holding (e, f, g, h); banks 1 and 3 (lanes
-// 4-7, 12-15) are "a-lanes" holding (a, b, c, d) of the record four lanes
-// below them.  Both halves run one instruction stream on registers X0..X3;
-// the lane constants select what it computes:
-//   S = rotr(X0, r1) ^ rotr(X0, r2) ^ rotr(X0, r3)   Sigma1(e) | Sigma0(a)
-//   u = m ? ~(X0 ^ X1) : X0;  C = u ? X1 : X2        Ch(e,f,g) | Maj(a,b,c)
-//   W = (X3 ^ m) + K  (+ partner's X3 on e-lanes)     h + W[t]+K[t] + d | -d
-//   V = S + C + W                                    e' | Sigma0 + Maj - d
+// Round waves: two lanes per record.  Within each 8-lane half row, lanes 0-3
+// are "e-lanes" holding (e, f, g, h) and lanes 4-7 "a-lanes" holding (a, b,
+// c, d); e-lane i and a-lane 7 - i hold one record (DPP row_half_mirror
+// swaps them).  Both halves run one instruction stream on registers X0..X3,
+// the a-half two rounds behind: in slot t the e-lanes do round t and the
+// a-lanes round t - 2.  A slot computes
+//   W = (X3 ^ m) + K + partner's X1                   h + W[t]+K[t] + d | e' - d
+//   S = rotr(X0, r1) ^ rotr(X0, r2) ^ rotr(X0, r3)    Sigma1(e) | Sigma0(a)
+//   u = m ? ~(X0 ^ X1) : X0;  C = u ? X1 : X2         Ch(e,f,g) | Maj(a,b,c)
+//   X0' = S + C + W                                    e' = d + T1 | a' = T1 + T2
 // with m = 0 and K = W[t]+K[t] on e-lanes, m = ~0 and K = 1 on a-lanes
-// (Maj(a,b,c) = ~(a^b) ? b : c bitwise; ~d + 1 = -d).  W needs only old
-// registers, so its DPP add stays off the critical path; one DPP add then
-// finishes the round: a-lanes take e' from their partner (a' = e' + Sigma0 +
-// Maj - d = T1 + T2).  That is 10 VALU per round against 14 for one lane
-// doing both halves.
-constexpr int kDppRowShl4 = 0x104;  // lane i reads lane i + 4 of its row
-constexpr int kDppRowShr4 = 0x114;  // lane i reads lane i - 4 of its row
+// (Maj(a,b,c) = ~(a^b) ? b : c bitwise; ~d + 1 = -d).  With the two-round
+// lag the partner's X1 is what each half needs: the a-lanes' X1 is a of
+// round t - 4, the e-lanes' d; the e-lanes' X1 is e' of round t - 2, the
+// round the a-lanes are on.  So one DPP add serves both halves, it reads a
+// register written two slots before, and a slot is 9 VALU whose only chain
+// is the rotations (or Ch/Maj) into one add3.  (Both halves on the same
+// round need a DPP add on the chain and a second one for d: 11 issue slots
+// a round against 9.)
+constexpr int kDppIdentity = 0xE4;    // quad_perm [0,1,2,3]: lane i reads itself
+constexpr int kDppHalfMirror = 0x141;  // lane i reads lane 7 - i of its half row
 constexpr int kEBanks = 0x5, kABanks = 0xA;
 
 struct ShaHalf {
@@ -1153,72 +1157,167 @@ __device__ __forceinline__ uint32_t rotr_v(uint32_t x, uint32_t n) { return __bu
 // from here on (no constant folding of lane masks, no reassociating sums).
 __device__ __forceinline__ void opaque(uint32_t& x) { asm("" : "+v"(x)); }
 
-__device__ __forceinline__ uint32_t from_a_partner(uint32_t x) {
-    return static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(x), kDppRowShl4, 0xF, kEBanks, false));
+template <int kCtrl, int kBanks>
+__device__ __forceinline__ uint32_t dpp_bits(uint32_t x) {
+    return static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(x), kCtrl, 0xF, kBanks, false));
 }
-
-__device__ __forceinline__ uint32_t from_e_partner(uint32_t x) {
-    return static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(x), kDppRowShr4, 0xF, kABanks, false));
-}
-
-// The 64 rounds of one block.  W is computed one round ahead and its first
-// term two rounds ahead, so the two instructions between V and the round's
-// DPP add are independent work (a DPP read waits two instructions after the
-// write of any register it reads).  The W+K words come from LDS four rounds
-// to a 16-byte read, each read issued kShaAhead quads (4 rounds a quad)
-// before its first use, so its latency hides behind the rounds before it.
-constexpr int kShaAhead = 2;
+// The partner's x.
+__device__ __forceinline__ uint32_t from_partner(uint32_t x) { return dpp_bits<kDppHalfMirror, 0xF>(x); }
+// The partner's x on e-lanes (from the a-lane), 0 on a-lanes; and the other way round.
+__device__ __forceinline__ uint32_t from_a_partner(uint32_t x) { return dpp_bits<kDppHalfMirror, kEBanks>(x); }
+__device__ __forceinline__ uint32_t from_e_partner(uint32_t x) { return dpp_bits<kDppHalfMirror, kABanks>(x); }
+// x on e-lanes, 0 on a-lanes; and the other way round.
+__device__ __forceinline__ uint32_t on_e_lanes(uint32_t x) { return dpp_bits<kDppIdentity, kEBanks>(x); }
+__device__ __forceinline__ uint32_t on_a_lanes(uint32_t x) { return dpp_bits<kDppIdentity, kABanks>(x); }
 
 __device__ __forceinline__ uint32_t quad_word(const u32x4& q, int t) {
     return (t & 3) == 0 ? q.x : (t & 3) == 1 ? q.y : (t & 3) == 2 ? q.z : q.w;
 }
 
-__device__ __forceinline__ void sha_rounds_pair(uint32_t x[4], const u32x4 (*slot)[kShaColumns], int column,
-                                                const ShaHalf& k) {
-    u32x4 q[kShaBlockQuads];
-#pragma unroll
-    for (int j = 0; j <= kShaAhead; ++j) q[j] = slot[j][column];
-    uint32_t x0 = x[0], x1 = x[1], x2 = x[2], x3 = x[3];
-    uint32_t z_next = (x2 ^ k.m) + quad_word(q[0], 1);  // round 1's X3 is X2 now
-    opaque(z_next);
-    uint32_t z = (x3 ^ k.m) + quad_word(q[0], 0);
-    opaque(z);
-    uint32_t w = from_a_partner(x3) + z;
+// Two-lane state between slots: X0..X3 as above and the chaining value, held
+// as E (the e-lanes' words) and F (the a-lanes' words).
+struct ShaLanes {
+    uint32_t x[4];
+    uint32_t e[4], f[4];
+};
+
+__device__ __forceinline__ uint32_t sha_sigma(uint32_t x0, const ShaHalf& k) {
+    return xor3(rotr_v(x0, k.r1), rotr_v(x0, k.r2), rotr_v(x0, k.r3));
+}
+
+// bitop3 tables index bits as (src0 << 2) | (src1 << 1) | src2.
+__device__ __forceinline__ uint32_t sha_choose(uint32_t x0, uint32_t x1, uint32_t x2, const ShaHalf& k) {
+    const uint32_t u = __builtin_amdgcn_bitop3_b32(x0, x1, k.m, 0xD2);  // m ? ~(x0 ^ x1) : x0
+    return __builtin_amdgcn_bitop3_b32(x1, x2, u, 0xE4);                // u ? x1 : x2
+}
+
+// One slot whose W has been summed but for S + C.
+__device__ __forceinline__ void sha_slot_finish(ShaLanes& l, uint32_t w, const ShaHalf& k) {
+    const uint32_t v = sha_sigma(l.x[0], k) + sha_choose(l.x[0], l.x[1], l.x[2], k) + w;
+    l.x[3] = l.x[2]; l.x[2] = l.x[1]; l.x[1] = l.x[0]; l.x[0] = v;
+}
+
+// A slot inside a block: one DPP add for both halves.
+__device__ __forceinline__ void sha_slot(ShaLanes& l, uint32_t word, const ShaHalf& k) {
+    uint32_t w = (l.x[3] ^ k.m) + word;
     opaque(w);
+    w = from_partner(l.x[1]) + w;
+    opaque(w);
+    sha_slot_finish(l, w, k);
+}
+
+// Slot 0 or 1 of a block: the e-lanes' rounds 0 and 1 of this block, the
+// a-lanes' rounds 62 and 63 of the previous one.  The e-lanes have fed
+// forward (their X holds this block's state) and the a-lanes have not: the
+// e-lanes' d is the a-lanes' X1 plus the chaining word not yet added (`fw`,
+// d then c), and the a-lanes' e' is the e-lanes' X1 before the feed-forward
+// (`unfed`: the slot before's X1 and X0).
+__device__ __forceinline__ void sha_slot_turn(ShaLanes& l, uint32_t word, uint32_t fw, uint32_t unfed,
+                                              const ShaHalf& k) {
+    uint32_t w = (l.x[3] ^ k.m) + word;
+    opaque(w);
+    w = from_a_partner(l.x[1] + fw) + w;
+    opaque(w);
+    w = from_e_partner(unfed) + w;
+    opaque(w);
+    sha_slot_finish(l, w, k);
+}
+
+// Between blocks: the e-lanes add their chaining words to X0..X3 and keep the
+// sums as the chaining words (a-lanes untouched); slots 0 and 1 finish the
+// previous block on the a-lanes, which then do the same with F.
+__device__ __forceinline__ void sha_block_turn(ShaLanes& l, uint32_t word0, uint32_t word1, const ShaHalf& k) {
+    const uint32_t unfed0 = l.x[0], unfed1 = l.x[1];
 #pragma unroll
-    for (int t = 0; t < 64; ++t) {
-        if ((t & 3) == 0 && (t >> 2) + kShaAhead + 1 < kShaBlockQuads)
-            q[(t >> 2) + kShaAhead + 1] = slot[(t >> 2) + kShaAhead + 1][column];
-        const uint32_t s = xor3(rotr_v(x0, k.r1), rotr_v(x0, k.r2), rotr_v(x0, k.r3));
-        // bitop3 tables index bits as (src0 << 2) | (src1 << 1) | src2.
-        const uint32_t u = __builtin_amdgcn_bitop3_b32(x0, x1, k.m, 0xD2);  // m ? ~(x0 ^ x1) : x0
-        const uint32_t c = __builtin_amdgcn_bitop3_b32(x1, x2, u, 0xE4);    // u ? x1 : x2
-        uint32_t v = s + c + w;  // e' | Sigma0 + Maj - d
-        opaque(v);
-        uint32_t z_after = 0;
-        if (t + 2 < 64) {
-            z_after = (x1 ^ k.m) + quad_word(q[(t + 2) >> 2], t + 2);  // h + W+K | -d of round t + 2
-            opaque(z_after);
+    for (int i = 0; i < 4; ++i) l.e[i] = l.x[i] = l.x[i] + on_e_lanes(l.e[i]);
+    sha_slot_turn(l, word0, l.f[3], unfed1, k);
+    sha_slot_turn(l, word1, l.f[2], unfed0, k);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) l.f[i] = l.x[i] = l.x[i] + on_a_lanes(l.f[i]);
+}
+
+// The W+K words come from LDS in batches of four 16-byte quads (16 rounds),
+// each batch read a whole batch ahead of its use and waited for with one
+// s_waitcnt: a wait costs a wave about 7 cycles however little it waits, so
+// one wait for 16 rounds rather than one for every 4.  A scheduling barrier
+// after the reads keeps them where they are issued; left to itself the
+// compiler sinks them to their first use, a batch later.
+constexpr int kShaBatch = 4;                                 // quads a batch
+constexpr int kShaBatches = kShaBlockQuads / kShaBatch;      // batches a block
+constexpr unsigned kWaitLds = 0xC07F;                        // s_waitcnt lgkmcnt(0)
+
+__device__ __forceinline__ void sha_read_batch(u32x4 dst[kShaBatch], const u32x4 (*slot)[kShaColumns], int batch,
+                                               int column) {
+#pragma unroll
+    for (int j = 0; j < kShaBatch; ++j) dst[j] = slot[kShaBatch * batch + j][column];
+    __builtin_amdgcn_sched_barrier(0);
+}
+
+// One block.  On entry the e-lanes hold the state after the previous block's
+// round 63 and the a-lanes after its round 61 (see sha_block_turn), and q[0]
+// holds this block's first W+K batch, not yet waited for; q[1] is free.  With
+// kNext the first batch of `next` is read during the last batch, into q[0].
+template <bool kNext>
+__device__ __forceinline__ void sha_block(ShaLanes& l, u32x4 (&q)[2][kShaBatch], const u32x4 (*slot)[kShaColumns],
+                                          const u32x4 (*next)[kShaColumns], int column, const ShaHalf& k) {
+#pragma unroll
+    for (int b = 0; b < kShaBatches; ++b) {
+        __builtin_amdgcn_s_waitcnt(kWaitLds);
+        if (b + 1 < kShaBatches)
+            sha_read_batch(q[(b + 1) & 1], slot, b + 1, column);
+        else if (kNext)
+            sha_read_batch(q[(b + 1) & 1], next, 0, column);
+        const u32x4* cur = q[b & 1];
+#pragma unroll
+        for (int t = 16 * b; t < 16 * b + 16; ++t) {
+            if (t == 0)
+                sha_block_turn(l, quad_word(cur[0], 0), quad_word(cur[0], 1), k);
+            else if (t > 1)
+                sha_slot(l, quad_word(cur[(t >> 2) & 3], t), k);
         }
-        if (t + 1 < 64) {
-            w = from_a_partner(x2) + z_next;  // e-lanes add their partner's d
-            opaque(w);
-        }
-        const uint32_t next = from_e_partner(v) + v;  // a' = e' + Sigma0 + Maj - d on a-lanes
-        x3 = x2; x2 = x1; x1 = x0; x0 = next;
-        z_next = z_after;
     }
-    x[0] += x0; x[1] += x1; x[2] += x2; x[3] += x3;
+}
+
+// The lanes' state before the first block of a launch, from chaining value
+// h[4] (the e-lanes' (e, f, g, h) or the a-lanes' (a, b, c, d)).  E = F = 0
+// makes the first feed-forwards copies.  The a-lanes have no rounds 62 and
+// 63 to finish, so they start as (c, d, y2, y3) with y3 and y2 chosen so that
+// slots 0 and 1 yield b and then a: slot 0 computes Sigma0(c) + Maj(c, d, y2)
+// + f - y3 and slot 1 Sigma0(b) + Maj(b, c, d) + e - y2, e and f being the
+// partner's X0 and X1 before the (here empty) feed-forward.  After them the
+// a-lanes hold (a, b, c, d).
+__device__ __forceinline__ ShaLanes sha_lanes_start(const uint32_t h[4], bool a_lane, const ShaHalf& k) {
+    ShaLanes l;
+    const uint32_t y2 = sha_sigma(h[1], k) + sha_choose(h[1], h[2], h[3], k) + from_e_partner(h[0]) - h[0];
+    const uint32_t y3 = sha_sigma(h[2], k) + sha_choose(h[2], h[3], y2, k) + from_e_partner(h[1]) - h[1];
+    l.x[0] = a_lane ? h[2] : h[0];
+    l.x[1] = a_lane ? h[3] : h[1];
+    l.x[2] = a_lane ? y2 : h[2];
+    l.x[3] = a_lane ? y3 : h[3];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) l.e[i] = l.f[i] = 0;
+    return l;
+}
+
+// After the last block: the e-lanes feed forward, the a-lanes run their
+// rounds 62 and 63 (K = 1) and feed forward; the chaining value is E on
+// e-lanes, F on a-lanes.
+__device__ __forceinline__ void sha_lanes_finish(ShaLanes& l, bool a_lane, const ShaHalf& k, uint32_t h[4]) {
+    sha_block_turn(l, 1u, 1u, k);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) h[i] = a_lane ? l.f[i] : l.e[i];
 }
 
 constexpr int kShaRoundWaves = 2;                  // round waves per workgroup, 32 records each
+constexpr int kShaProducers = 2;                   // message-schedule waves, alternate blocks of a step
 constexpr int kShaRecords = 32 * kShaRoundWaves;   // records per workgroup
-constexpr int kShaThreads = 64 * (kShaRoundWaves + 1);  // the round waves, then the message-schedule wave
-constexpr int kShaStep = 4;  // blocks per barrier; the producer fills one half while the rounds read the other
+constexpr int kShaThreads = 64 * (kShaRoundWaves + kShaProducers);  // the round waves, then the producers
+constexpr int kShaStep = 4;  // blocks per barrier; the producers fill one half while the rounds read the other
+constexpr int kShaProducerBlocks = kShaStep / kShaProducers;  // blocks of a step per producer
 
-// The producer's step for block `blk`: expand the words loaded for it, then
+// A producer's step for block `blk`: expand the words loaded for it, then
 // start the loads of block blk + kShaStep into the same registers.  Each of
-// the kShaStep register sets is loaded a whole step ahead of its expansion.
+// a producer's register sets is loaded a whole step ahead of its expansion.
 template <bool kAligned>
 __device__ __forceinline__ void sha_produce(const uint8_t* __restrict__ p, uint64_t record_bytes, uint64_t whole,
                                             int nfinal, uint64_t nblocks, uint64_t blk, uint32_t raw[16],
@@ -1243,12 +1342,15 @@ __device__ __forceinline__ void sha256_group(ShaSchedule& sched, const uint8_t* 
                                              uint64_t record_bytes, uint64_t pitch, int64_t n_records, uint64_t b0,
                                              uint64_t b1, uint32_t* __restrict__ state, uint32_t* __restrict__ out,
                                              int64_t group) {
-    const bool producer = threadIdx.x >= 64 * kShaRoundWaves;
+    const int wave = threadIdx.x >> 6;
+    const bool producer = wave >= kShaRoundWaves;
+    const int part = wave - kShaRoundWaves;  // a producer's blocks of a step: part, part + kShaProducers, ...
     const int lane = threadIdx.x & 63;
-    const int bank = (lane >> 2) & 3;
-    const bool a_lane = bank & 1;
+    const bool a_lane = (lane >> 2) & 1;
     // Record of this lane within the workgroup's kShaRecords (producer lanes past them idle).
-    const int rec = producer ? lane : (threadIdx.x >> 6) * 32 + (lane >> 4) * 8 + (bank >> 1) * 4 + (lane & 3);
+    // Round lanes: e-lane i and a-lane 7 - i of each 8-lane half row share a record.
+    const int rec = producer ? lane
+                             : wave * 32 + (lane >> 3) * 4 + (a_lane ? 3 - (lane & 3) : (lane & 3));
     const int64_t r = group * kShaRecords + rec;
     const bool live = rec < kShaRecords && r < n_records;
     // Lanes past the last record hash record 0 (in bounds) and store nothing.
@@ -1258,55 +1360,72 @@ __device__ __forceinline__ void sha256_group(ShaSchedule& sched, const uint8_t* 
     const uint64_t nblocks = whole + nfinal;
     const uint64_t span = b1 - b0;
     const uint64_t steps = (span + kShaStep - 1) / kShaStep;
-    uint32_t raw[kShaStep][16];
+    uint32_t raw[kShaProducerBlocks][16];
     if (producer) {
-        for (int i = lane; i < 2 * kShaStep * kShaBlockQuads; i += 64) {
+        for (int i = lane + 64 * part; i < 2 * kShaStep * kShaBlockQuads; i += 64 * kShaProducers) {
             const int slot = i / kShaBlockQuads;
             sched[slot / kShaStep][slot % kShaStep][i % kShaBlockQuads][64] = u32x4{1u, 1u, 1u, 1u};
         }
 #pragma unroll
-        for (int i = 0; i < kShaStep; ++i)
-            if (static_cast<uint64_t>(i) < span) sha_message_raw<kAligned>(p, record_bytes, whole, nfinal, b0 + i, raw[i]);
+        for (int j = 0; j < kShaProducerBlocks; ++j) {
+            const int i = part + kShaProducers * j;
+            if (static_cast<uint64_t>(i) < span) sha_message_raw<kAligned>(p, record_bytes, whole, nfinal, b0 + i, raw[j]);
+        }
 #pragma unroll
-        for (int i = 0; i < kShaStep; ++i)
+        for (int j = 0; j < kShaProducerBlocks; ++j) {
+            const int i = part + kShaProducers * j;
             if (static_cast<uint64_t>(i) < span)
-                sha_produce<kAligned>(p, record_bytes, whole, nfinal, b1, b0 + i, raw[i], sched[0][i], lane);
+                sha_produce<kAligned>(p, record_bytes, whole, nfinal, b1, b0 + i, raw[j], sched[0][i], lane);
+        }
     }
     __syncthreads();
     ShaHalf half = a_lane ? ShaHalf{2, 13, 22, ~0u} : ShaHalf{6, 11, 25, 0u};
     opaque(half.m);
-    uint32_t x[4];
+    uint32_t h[4];
     uint32_t* chain = state ? state + 8 * (live ? r : 0) + (a_lane ? 0 : 4) : nullptr;
     if (b0 > 0) {
-        const u32x4 h = *reinterpret_cast<const u32x4*>(chain);
-        x[0] = h.x; x[1] = h.y; x[2] = h.z; x[3] = h.w;
+        const u32x4 v = *reinterpret_cast<const u32x4*>(chain);
+        h[0] = v.x; h[1] = v.y; h[2] = v.z; h[3] = v.w;
     } else if (a_lane) {
-        x[0] = 0x6a09e667; x[1] = 0xbb67ae85; x[2] = 0x3c6ef372; x[3] = 0xa54ff53a;
+        h[0] = 0x6a09e667; h[1] = 0xbb67ae85; h[2] = 0x3c6ef372; h[3] = 0xa54ff53a;
     } else {
-        x[0] = 0x510e527f; x[1] = 0x9b05688c; x[2] = 0x1f83d9ab; x[3] = 0x5be0cd19;
+        h[0] = 0x510e527f; h[1] = 0x9b05688c; h[2] = 0x1f83d9ab; h[3] = 0x5be0cd19;
     }
+    ShaLanes l = sha_lanes_start(h, a_lane, half);
     const int column = a_lane ? 64 : rec;
+    u32x4 q[2][kShaBatch];  // W+K batches, read into alternately
     for (uint64_t step = 0; step < steps; ++step) {
         const uint64_t first = b0 + step * kShaStep;
         if (producer) {
 #pragma unroll
-            for (int i = 0; i < kShaStep; ++i)
+            for (int j = 0; j < kShaProducerBlocks; ++j) {
+                const int i = part + kShaProducers * j;
                 if (first + kShaStep + i < b1)
-                    sha_produce<kAligned>(p, record_bytes, whole, nfinal, b1, first + kShaStep + i, raw[i],
+                    sha_produce<kAligned>(p, record_bytes, whole, nfinal, b1, first + kShaStep + i, raw[j],
                                           sched[(step + 1) & 1][i], lane);
+            }
         } else {
+            sha_read_batch(q[0], sched[step & 1][0], 0, column);
 #pragma unroll
-            for (int i = 0; i < kShaStep; ++i)
-                if (first + i < b1) sha_rounds_pair(x, sched[step & 1][i], column, half);
+            for (int i = 0; i < kShaStep; ++i) {
+                if (first + i >= b1) break;
+                if (i + 1 < kShaStep)
+                    sha_block<true>(l, q, sched[step & 1][i], sched[step & 1][i + 1], column, half);
+                else
+                    sha_block<false>(l, q, sched[step & 1][i], nullptr, column, half);
+            }
         }
         __syncthreads();
     }
-    if (!producer && live) {
-        if (b1 == nblocks)
-            *reinterpret_cast<u32x4*>(out + 8 * r + (a_lane ? 0 : 4)) =
-                u32x4{bswap(x[0]), bswap(x[1]), bswap(x[2]), bswap(x[3])};
-        else
-            *reinterpret_cast<u32x4*>(chain) = u32x4{x[0], x[1], x[2], x[3]};
+    if (!producer) {
+        sha_lanes_finish(l, a_lane, half, h);
+        if (live) {
+            if (b1 == nblocks)
+                *reinterpret_cast<u32x4*>(out + 8 * r + (a_lane ? 0 : 4)) =
+                    u32x4{bswap(h[0]), bswap(h[1]), bswap(h[2]), bswap(h[3])};
+            else
+                *reinterpret_cast<u32x4*>(chain) = u32x4{h[0], h[1], h[2], h[3]};
+        }
     }
 }
 
