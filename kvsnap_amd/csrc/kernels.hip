@@ -588,24 +588,59 @@ __device__ __forceinline__ void crc_fold_rest(const uint32_t* lds, uint32_t cols
 }
 
 // The LDS tables of a CRC workgroup: H shared at byte 0, then the lanes'
-// private copies of Gn and of S.
-__device__ __forceinline__ void crc_fill_tables(uint32_t* lds) {
-    // Thread t owns S entry t (table t / 256, value t % 256): one read, then its 32 lane columns are one
-    // 128-byte run of the private layout, written as eight 16-byte stores.
-    static_assert(kCrcThreads == 4 * 256, "one thread per table entry");
-    const uint32_t t = threadIdx.x, table = t >> 8, v = t & 255u;
-    const uint32_t word = g_crc_tables[t];
-    const u32x4 four = {word, word, word, word};
-    u32x4* run = reinterpret_cast<u32x4*>(reinterpret_cast<char*>(lds + kCrcSAt) + (table >> 1) * 65536u +
-                                          v * 256u + (table & 1u) * 128u);
+// private copies of Gn and of S.  S entry (table, v) is a 128-byte run (its
+// 32 lane columns) at (table / 2) * 64 KiB + v * 256 + (table % 2) * 128.
+// The fill writes S as 16-byte chunks in address order, chunk k * 1024 + t
+// from thread t, so the 64 lanes of each write cover 1 KiB of consecutive
+// banks; one lane per entry (its run's eight chunks) put a wave's lanes 256
+// bytes apart, all on the same four banks, and took about 4 us a launch.
+// Gn is written eight threads per entry (128 consecutive bytes), H one word
+// per thread.
+constexpr int kCrcFillChunks = kCrcPrivateBytes / 16 / kCrcThreads;  // S chunks per thread
+
+struct CrcTableWords {
+    uint32_t s[kCrcFillChunks], advance, behind;
+};
+
+__device__ __forceinline__ uint32_t crc_fill_entry(uint32_t chunk) {
+    const uint32_t half = chunk >> 12, r = chunk & 4095u;
+    return (2u * half + ((r >> 3) & 1u)) * 256u + (r >> 4);  // table * 256 + v
+}
+
+__device__ __forceinline__ CrcTableWords crc_table_words() {
+    static_assert(kCrcThreads == 4 * 256, "one thread per H entry");
+    static_assert(kCrcFillChunks * kCrcThreads * 16 == kCrcPrivateBytes, "S chunks split evenly");
+    const uint32_t t = threadIdx.x;
+    CrcTableWords w;
 #pragma unroll
-    for (int k = 0; k < 8; ++k) run[k] = four;
-    // Eight threads per Gn entry (table e / 16, value e % 16), four lane columns (16 bytes) each.
+    for (int k = 0; k < kCrcFillChunks; ++k) w.s[k] = g_crc_tables[crc_fill_entry(k * kCrcThreads + t)];
+    w.advance = g_crc_tables[kCrcAdvance + (t >> 3)];
+    w.behind = g_crc_tables[kCrcBehind + t];
+    return w;
+}
+
+__device__ __forceinline__ void crc_fill_tables(uint32_t* lds, const CrcTableWords& w) {
+    const uint32_t t = threadIdx.x;
+    u32x4* chunks = reinterpret_cast<u32x4*>(lds + kCrcSAt);
+#pragma unroll
+    for (int k = 0; k < kCrcFillChunks; ++k) chunks[k * kCrcThreads + t] = u32x4{w.s[k], w.s[k], w.s[k], w.s[k]};
     const uint32_t e = t >> 3, nib_table = e >> 4, nib = e & 15u;
-    const uint32_t adv = g_crc_tables[kCrcAdvance + e];
     *reinterpret_cast<u32x4*>(reinterpret_cast<char*>(lds + kCrcGnAt) + (nib_table >> 1) * 4096u + nib * 256u +
-                              (nib_table & 1u) * 128u + (t & 7u) * 16u) = u32x4{adv, adv, adv, adv};
-    lds[t] = g_crc_tables[kCrcBehind + t];
+                              (nib_table & 1u) * 128u + (t & 7u) * 16u) =
+        u32x4{w.advance, w.advance, w.advance, w.advance};
+    lds[t] = w.behind;
+}
+
+// The workgroup's tables are written: wait for this wave's LDS writes and
+// meet the other waves, without waiting for the record loads in flight (a
+// __syncthreads would, and every wave would then start folding only when the
+// slowest of the workgroup's first batches had landed).  The empty asm
+// statements keep the compiler from moving memory accesses across.
+__device__ __forceinline__ void crc_tables_ready() {
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0); vmcnt and expcnt left alone
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
 }
 
 // Groups of padding only (in stripe 0) are skipped, not folded: the registers are still zero there.
@@ -720,13 +755,15 @@ __global__ __launch_bounds__(kCrcThreads) void crc_stripes_kernel(const uint8_t*
     };
     uint32_t lane_shift, cols;
     {
-        // The first job's first batch is in flight while the tables are filled.
+        // The table words are read first, then the first job's first batch, which is in flight while the
+        // tables are filled.
+        const CrcTableWords words = crc_table_words();
+        lane_shift = g_crc_tables[kCrcLaneShift + lane];
         u32x4 a[kCrcBatchWords];
         if (first < jobs) crc_stripe_first<kAligned>(job_record(first), job_start(first), groups, lane, a);
-        crc_fill_tables(lds);
-        lane_shift = g_crc_tables[kCrcLaneShift + lane];
+        crc_fill_tables(lds, words);
         cols = crc_columns(lane);
-        __syncthreads();
+        crc_tables_ready();
         if (first < jobs) {
             const uint32_t x =
                 crc_stripe_rest<kAligned>(lds, lane, cols, lane_shift, job_record(first), job_start(first), groups, a);
@@ -800,17 +837,19 @@ __global__ __launch_bounds__(kCrcThreads) void crc_records_kernel(const uint8_t*
     const int64_t stride = static_cast<int64_t>(gridDim.x) * per_group;
     uint32_t lane_shift, cols;
     {
-        // The first round's first batch is in flight while the tables are filled.
+        // The table words are read first, then the first round's first batch, which is in flight while the
+        // tables are filled.
+        const CrcTableWords words = crc_table_words();
+        lane_shift = g_crc_tables[kCrcLaneShift + lane];
         u32x4 a[kCrcBatchWords];
         const int rec_in_round = wave / stripes, j = wave - rec_in_round * stripes;
         if (rec_in_round < per_group && first + rec_in_round < n_records)
             crc_stripe_first<kAligned>(records + (first + rec_in_round) * pitch,
                                        static_cast<int64_t>(j) * groups * kCrcGroup - static_cast<int64_t>(pad),
                                        groups, lane, a);
-        crc_fill_tables(lds);
-        lane_shift = g_crc_tables[kCrcLaneShift + lane];
+        crc_fill_tables(lds, words);
         cols = crc_columns(lane);
-        __syncthreads();
+        crc_tables_ready();
         if (first < n_records)  // workgroup-uniform
             crc_records_round<kAligned>(lds, stripe_crc, lane, cols, lane_shift, wave, records, pitch, n_records,
                                         stripes, groups, pad, powers, init_term, out, first, a, true);
