@@ -187,13 +187,23 @@ S_SELECTORS = (0x0C0C0400, 0x0C0C0501, 0x0C020600, 0x0C020701)
 GN_LOOKUPS = [(page, half, 0x0C0C0000 | ((4 + page) << 8) | half) for page in range(4) for half in (0, 1)]
 
 
+def fill_entry(chunk):
+    """(table, v) of the S entry whose four lane columns the fill writes as 16-byte chunk `chunk`."""
+    half, r = chunk >> 12, chunk & 4095
+    return 2 * half + ((r >> 3) & 1), r >> 4
+
+
 def filled_lds():
     """The bytes crc_fill_tables writes: {byte address: table word}."""
     lds = {}
-    for t in range(1024):                               # S entry t, its 32 lane columns
-        table, v = t >> 8, t & 255
-        for k in range(32):
-            lds[S_AT + (table >> 1) * 65536 + v * 256 + (table & 1) * 128 + 4 * k] = S[table][v]
+    for k in range(8):                                  # S: thread t writes chunk k * 1024 + t
+        for t in range(1024):
+            chunk = k * 1024 + t
+            table, v = fill_entry(chunk)
+            for j in range(4):
+                assert S_AT + 16 * chunk + 4 * j not in lds
+                lds[S_AT + 16 * chunk + 4 * j] = S[table][v]
+    for t in range(1024):
         e = t >> 3                                      # Gn entry e, four lane columns
         nib_table, nib = e >> 4, e & 15
         for k in range(4):
@@ -201,6 +211,14 @@ def filled_lds():
                 GN[nib_table][nib]
         lds[4 * t] = H[t >> 8][t & 255]
     return lds
+
+
+def test_each_wave_write_of_the_s_fill_covers_one_kib_of_consecutive_banks():
+    for k in range(8):
+        for wave in range(16):
+            chunks = [k * 1024 + 64 * wave + lane for lane in range(64)]
+            assert chunks == list(range(chunks[0], chunks[0] + 64))      # 1 KiB contiguous
+            assert {(4 * c + j) % 32 for c in chunks[:8] for j in range(4)} == set(range(32))  # 8 lanes, 32 banks
 
 
 def test_the_private_tables_fill_the_lds_once_and_every_lane_reads_its_own_bank_and_entry():
