@@ -1732,6 +1732,15 @@ uint32_t* static_crc_workspace() {
     return g_scratch_ptr[device];
 }
 
+// LDS a link-bound copy workgroup asks for and does not use.  With it no CU
+// can hold one of these workgroups beside a SHA-256 workgroup (133,120 of the
+// CU's 163,840 bytes), so the dispatcher keeps the copies off the hash
+// chains' CUs: a copy wave on a SIMD beside a round wave slows the chain
+// (SHA-256 range launches took 2.5-3.5 ms beside the restore kernel, 1.8 ms
+// alone).  The copies wait on the host link, not on their CUs.
+constexpr unsigned kCopyLdsFence = 32 * 1024;
+static_assert(kCopyLdsFence + sizeof(ShaSchedule) > 160 * 1024, "a copy and a SHA workgroup must not share a CU");
+
 }  // namespace
 
 extern "C" {
@@ -1749,7 +1758,7 @@ int kvsnap_restore_blocks(const int64_t* sources, const int64_t* blocks, int64_t
             throw std::runtime_error("restore tables must be device pointers");
         const CopyShape shape = copy_shape(kRestoreThreads, kRestoreUnroll, n_blocks * n_spans, min_span_bytes,
                                            programs);
-        hipLaunchKernelGGL(restore_kernel, dim3(shape.grid), dim3(kRestoreThreads), 0,
+        hipLaunchKernelGGL(restore_kernel, dim3(shape.grid), dim3(kRestoreThreads), kCopyLdsFence,
                            reinterpret_cast<hipStream_t>(stream), sources, blocks, n_blocks, span_offsets,
                            span_bases, span_pitches, span_words, n_spans, shape.lane_shift);
         check_launch("restore");
@@ -1769,7 +1778,7 @@ int kvsnap_restore_blocks_checked(const int64_t* sources, const int64_t* blocks,
         ensure_crc_tables();
         constexpr int64_t waves = kRestoreThreads / 64;
         const unsigned grid = grid_for((n_blocks * n_spans + waves - 1) / waves, programs);
-        hipLaunchKernelGGL(restore_checked_kernel, dim3(grid), dim3(kRestoreThreads), 0,
+        hipLaunchKernelGGL(restore_checked_kernel, dim3(grid), dim3(kRestoreThreads), kCopyLdsFence,
                            reinterpret_cast<hipStream_t>(stream), sources, blocks, n_blocks, span_offsets,
                            span_bases, span_pitches, span_words, n_spans, partial);
         check_launch("checked restore");
@@ -1843,7 +1852,7 @@ int kvsnap_gather_to_records(const int64_t* dests, const int64_t* blocks, int64_
             throw std::runtime_error("gather tables must be device pointers");
         const CopyShape shape = copy_shape(kRestoreThreads, kRestoreUnroll, n_blocks * n_spans, min_span_bytes,
                                            programs);
-        hipLaunchKernelGGL(gather_to_kernel, dim3(shape.grid), dim3(kRestoreThreads), 0,
+        hipLaunchKernelGGL(gather_to_kernel, dim3(shape.grid), dim3(kRestoreThreads), kCopyLdsFence,
                            reinterpret_cast<hipStream_t>(stream), dests, blocks, n_blocks, span_offsets, span_bases,
                            span_pitches, span_words, n_spans, shape.lane_shift);
         check_launch("gather to records");
