@@ -1354,18 +1354,38 @@ constexpr int kShaThreads = 64 * (kShaRoundWaves + kShaProducers);  // the round
 constexpr int kShaStep = 4;  // blocks per barrier; the producers fill one half while the rounds read the other
 constexpr int kShaProducerBlocks = kShaStep / kShaProducers;  // blocks of a step per producer
 
-// A producer's step for block `blk`: expand the words loaded for it, then
-// start the loads of block blk + kShaStep into the same registers.  Each of
-// a producer's register sets is loaded a whole step ahead of its expansion.
+// A producer's step for block `blk` (of blocks below `end`): expand the words
+// loaded for it, then start the loads of block blk + kShaAheadSteps *
+// kShaStep into the same registers.  A producer keeps kShaAheadSteps register
+// sets per block of a step, so each block's loads are in flight for two whole
+// steps (about 10 us) before its expansion: beside a restore kernel's reads
+// of host memory, loads issued one step ahead came back late and the round
+// waves waited at the step barrier (58 cycles a round against 45).
+constexpr int kShaAheadSteps = 2;
+
 template <bool kAligned>
 __device__ __forceinline__ void sha_produce(const uint8_t* __restrict__ p, uint64_t record_bytes, uint64_t whole,
-                                            int nfinal, uint64_t nblocks, uint64_t blk, uint32_t raw[16],
+                                            int nfinal, uint64_t end, uint64_t blk, uint32_t raw[16],
                                             u32x4 (*slot)[kShaColumns], int lane) {
     uint32_t w[16];
 #pragma unroll
     for (int i = 0; i < 16; ++i) w[i] = bswap(raw[i]);
-    if (blk + kShaStep < nblocks) sha_message_raw<kAligned>(p, record_bytes, whole, nfinal, blk + kShaStep, raw);
+    const uint64_t next = blk + kShaAheadSteps * kShaStep;
+    if (next < end) sha_message_raw<kAligned>(p, record_bytes, whole, nfinal, next, raw);
     sha_schedule(w, slot, lane);
+}
+
+// The register sets of the next two steps' blocks trade places.
+__device__ __forceinline__ void sha_rotate_sets(uint32_t (&raw)[kShaAheadSteps][kShaProducerBlocks][16]) {
+    static_assert(kShaAheadSteps == 2, "two sets");
+#pragma unroll
+    for (int j = 0; j < kShaProducerBlocks; ++j)
+#pragma unroll
+        for (int k = 0; k < 16; ++k) {
+            const uint32_t t = raw[0][j][k];
+            raw[0][j][k] = raw[1][j][k];
+            raw[1][j][k] = t;
+        }
 }
 
 using ShaSchedule = u32x4[2][kShaStep][kShaBlockQuads][kShaColumns];
@@ -1399,23 +1419,27 @@ __device__ __forceinline__ void sha256_group(ShaSchedule& sched, const uint8_t* 
     const uint64_t nblocks = whole + nfinal;
     const uint64_t span = b1 - b0;
     const uint64_t steps = (span + kShaStep - 1) / kShaStep;
-    uint32_t raw[kShaProducerBlocks][16];
+    // raw[0]: the words of the producer's blocks of the next step to expand; raw[1]: of the step after.
+    uint32_t raw[kShaAheadSteps][kShaProducerBlocks][16];
     if (producer) {
         for (int i = lane + 64 * part; i < 2 * kShaStep * kShaBlockQuads; i += 64 * kShaProducers) {
             const int slot = i / kShaBlockQuads;
             sched[slot / kShaStep][slot % kShaStep][i % kShaBlockQuads][64] = u32x4{1u, 1u, 1u, 1u};
         }
 #pragma unroll
-        for (int j = 0; j < kShaProducerBlocks; ++j) {
-            const int i = part + kShaProducers * j;
-            if (static_cast<uint64_t>(i) < span) sha_message_raw<kAligned>(p, record_bytes, whole, nfinal, b0 + i, raw[j]);
-        }
+        for (int a = 0; a < kShaAheadSteps; ++a)
+#pragma unroll
+            for (int j = 0; j < kShaProducerBlocks; ++j) {
+                const uint64_t i = static_cast<uint64_t>(a * kShaStep + part + kShaProducers * j);
+                if (i < span) sha_message_raw<kAligned>(p, record_bytes, whole, nfinal, b0 + i, raw[a][j]);
+            }
 #pragma unroll
         for (int j = 0; j < kShaProducerBlocks; ++j) {
             const int i = part + kShaProducers * j;
             if (static_cast<uint64_t>(i) < span)
-                sha_produce<kAligned>(p, record_bytes, whole, nfinal, b1, b0 + i, raw[j], sched[0][i], lane);
+                sha_produce<kAligned>(p, record_bytes, whole, nfinal, b1, b0 + i, raw[0][j], sched[0][i], lane);
         }
+        sha_rotate_sets(raw);
     }
     __syncthreads();
     ShaHalf half = a_lane ? ShaHalf{2, 13, 22, ~0u} : ShaHalf{6, 11, 25, 0u};
@@ -1440,9 +1464,10 @@ __device__ __forceinline__ void sha256_group(ShaSchedule& sched, const uint8_t* 
             for (int j = 0; j < kShaProducerBlocks; ++j) {
                 const int i = part + kShaProducers * j;
                 if (first + kShaStep + i < b1)
-                    sha_produce<kAligned>(p, record_bytes, whole, nfinal, b1, first + kShaStep + i, raw[j],
+                    sha_produce<kAligned>(p, record_bytes, whole, nfinal, b1, first + kShaStep + i, raw[0][j],
                                           sched[(step + 1) & 1][i], lane);
             }
+            sha_rotate_sets(raw);
         } else {
             sha_read_batch(q[0], sched[step & 1][0], 0, column);
 #pragma unroll
