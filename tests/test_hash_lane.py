@@ -5,9 +5,9 @@ fills a record set's digests (hashlib over host memory) and CRC32Cs (the
 oracle) when a range ends its chain, and can fail a chosen launch.  The GPU
 tests check the chaining state between ranges against hashlib; these check
 that the lane merges jobs into shared launches, advances each job by its
-own ranges, carries at most eight jobs a launch, reports a failed launch to
-every job in it and keeps serving later ones, and finishes every job before
-``close`` returns.
+own ranges, carries at most eight jobs a launch, reports a failed launch (or
+a kernel library that fails to load) to every job in it and keeps serving
+later ones, and finishes every job before ``close`` returns.
 """
 import ctypes as C
 from contextlib import nullcontext
@@ -208,3 +208,23 @@ def test_close_finishes_every_job_and_refuses_new_ones():
             check_digests(job, records)
         with pytest.raises(RuntimeError, match="closed"):
             submit(lane, record_sets(1, seed=7))
+
+
+def test_a_library_that_fails_to_load_fails_the_jobs_and_the_lane_serves_the_next():
+    fake, calls = FakeLibrary(), []
+
+    def library(library=None):          # the lane thread's first load fails
+        if threading.current_thread().name == "kvsnap-hash":
+            calls.append(1)
+            if len(calls) == 1:
+                raise RuntimeError("HIP dataplane library not built")
+        return fake
+
+    with patch.object(dataplane, "kernel_library", library):
+        lane = HashLane(FakeTorch(), SimpleNamespace(cuda_stream=7, synchronize=lambda: None))
+        first = submit(lane, record_sets(1, seed=8))[0]
+        with pytest.raises(RuntimeError, match="not built"):
+            first.synchronize()
+        later = record_sets(1, seed=9)
+        check_digests(submit(lane, later)[0], later[0])
+        lane.close()
