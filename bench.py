@@ -419,7 +419,10 @@ def run_save_restore(args):
     log(f"parity: restore byte-exact={exact}, CRC32C+SHA-256 bit-exact={digests_exact}")
 
     gather, restore, crc, sha = kernels["gather"], kernels["restore"], kernels["crc32c"], kernels["sha256"]
-    gather_achieved = 2 * total / (gather["avg_ms"] * 1e6)          # read + write, one launch per save
+    # Read + write of every record, over the save's gather launches: the first chunk's on the copy stream
+    # and the rest's on the lead stream (one launch where the plane has no lead stream).
+    gather_per_save = gather["launches"] // args.steps
+    gather_achieved = 2 * total * args.steps / (gather["total_ms"] * 1e6)
     restore_link = (total * instrumented_steps / restore["launches"]) / (restore["avg_ms"] * 1e6)
     # After the timed region, on the session's records gathered into device memory: the scatter (the
     # verified restore's last step) into the restore targets, which already hold the same bytes, and the
@@ -490,11 +493,13 @@ def run_save_restore(args):
         "pcie5_x16_gbps": PCIE5_X16_GBPS,
         "restore_frac_of_pcie5_x16": round(total / lat["restore"] / 1e6 / PCIE5_X16_GBPS, 4),
         "save_frac_of_pcie5_x16": round(total / lat["save"] / 1e6 / PCIE5_X16_GBPS, 4),
-        "kernels_ms": {name: round(k["avg_ms"], 4) for name, k in kernels.items()},
-        "kernels_ms_source": "gather: HIP events in the timed steps; the others: 3 steps after them with every "
-                             "launch timed",
+        "kernels_ms": {name: round(k["total_ms"] / args.steps if name == "gather" else k["avg_ms"], 4)
+                       for name, k in kernels.items()},
+        "kernels_ms_source": "gather: HIP events in the timed steps, summed over a save's launches; the others: "
+                             "3 steps after them with every launch timed, per launch",
         "roofline": {"kernel": "gather_kernel", "bound": "hbm", "achieved": round(gather_achieved, 1),
                      "peak": HBM_PEAK_GBPS, "unit": "GB/s", "frac": round(gather_achieved / HBM_PEAK_GBPS, 4),
+                     "launches_per_save": gather_per_save,
                      "traffic": measured_traffic("gather_kernel"), "algorithmic_bytes": 2 * total,
                      "traffic_source": "profiles/qwen3-8b-8k-kernels.traffic.md (rocprofv3 FETCH_SIZE, WRITE_SIZE)"},
         "link_roofline": {"kernel": "restore_kernel", "bound": "host-link", "achieved": round(restore_link, 2),
