@@ -497,14 +497,14 @@ def run_save_restore(args):
                        for name, k in kernels.items()},
         "kernels_ms_source": "gather: HIP events in the timed steps, summed over a save's launches; the others: "
                              "3 steps after them with every launch timed, per launch",
-        "roofline": {"kernel": "gather_kernel", "bound": "hbm", "achieved": round(gather_achieved, 1),
+        "roofline": {"kernel": "gather_pieces_kernel", "bound": "hbm", "achieved": round(gather_achieved, 1),
                      "peak": HBM_PEAK_GBPS, "unit": "GB/s", "frac": round(gather_achieved / HBM_PEAK_GBPS, 4),
                      "launches_per_save": gather_per_save,
-                     "traffic": measured_traffic("gather_kernel"), "algorithmic_bytes": 2 * total,
+                     "traffic": measured_traffic("gather_pieces_kernel"), "algorithmic_bytes": 2 * total,
                      "traffic_source": "profiles/qwen3-8b-8k-kernels.traffic.md (rocprofv3 FETCH_SIZE, WRITE_SIZE)"},
         "link_roofline": {"kernel": "restore_kernel", "bound": "host-link", "achieved": round(restore_link, 2),
                           "peak": round(h2d_peak, 2), "unit": "GB/s", "frac": round(restore_link / h2d_peak, 4)},
-        "scatter_roofline": {"kernel": "scatter_kernel (device records to cache)", "bound": "hbm",
+        "scatter_roofline": {"kernel": "scatter_pieces_kernel (device records to cache)", "bound": "hbm",
                              "achieved": round(scatter_achieved, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                              "frac": round(scatter_achieved / HBM_PEAK_GBPS, 4), "ms": round(scatter_ms, 4)},
         "crc_roofline": {"kernel": "crc_records_kernel", "bound": "hbm", "achieved": round(crc_achieved, 1),
@@ -943,17 +943,17 @@ def run_kernels(args):
     hint = plane.min_span_bytes
     runs = {
         "plain_copy": (lambda: other.copy_(stage), 2 * total, args.reps),
-        "gather_kernel": (lambda: gather_blocks(ids, *tables, stage.data_ptr(), size, min_span_bytes=hint),
-                          2 * total, args.reps),
+        "gather_pieces_kernel": (lambda: gather_blocks(ids, *tables, stage.data_ptr(), size, min_span_bytes=hint),
+                                 2 * total, args.reps),
         # 512 records take the one-launch plan (crc_records_kernel: stripes combined in the workgroup).
         "crc_records_kernel": (lambda: _check(lib, lib.kvsnap_crc32c_records(
             stage.data_ptr(), size, size, session, 0, crc.data_ptr(), work.data_ptr(), work_bytes,
             stream.cuda_stream)), total, args.reps),
         "restore_kernel": (lambda: copy_host_blocks(pinned, dst, *tables, min_span_bytes=hint), 2 * total,
                            args.reps),
-        # The verified restore's scatter: records in device staging, one workgroup per (block, span).
-        "scatter_kernel": (lambda: scatter_blocks(stage.data_ptr(), size, dst, *tables, min_span_bytes=hint),
-                           2 * total, args.reps),
+        # The copy-engine restore's scatter: records in device staging, one wave per KiB of a span.
+        "scatter_pieces_kernel": (lambda: scatter_blocks(stage.data_ptr(), size, dst, *tables,
+                                                         min_span_bytes=hint), 2 * total, args.reps),
         "sha256_kernel": (lambda: _check(lib, lib.kvsnap_sha256_records(
             stage.data_ptr(), size, size, session, sha.data_ptr(), stream.cuda_stream)), total, 1),
     }

@@ -111,13 +111,15 @@ __device__ __forceinline__ JobLanes job_lanes(int lane_shift) {
 // workgroups with 8 loads in flight per lane keeps it full while leaving the
 // CUs to the engine.
 constexpr int kRestoreThreads = 256, kRestoreUnroll = 8;
-// Gather: HBM to HBM, 1024-lane workgroups with 4 loads in flight per lane
-// (64 KiB per pass), the fastest shape measured.  A 32 KiB span takes the
-// whole workgroup, 2 loads per lane.  Tried and slower on the 8k Qwen3-8B
-// gather: an unroll of 8 (512 lanes per span, 4 loads each; 106 SGPRs, one
-// workgroup per CU: 5.1 against 5.9 TB/s), and global-address-space loads
-// and stores in place of the flat ones the table addresses compile to (equal
-// on 32 KiB spans, 5.6 against 5.9 TB/s on 64 KiB ones).
+// Gather with a fixed grid or an unknown span length (the pieces kernel below
+// takes the rest): HBM to HBM, 1024-lane workgroups with 4 loads in flight
+// per lane (64 KiB per pass), the fastest shape of this kind measured.  A
+// 32 KiB span takes the whole workgroup, 2 loads per lane.  Tried and slower
+// on the 8k Qwen3-8B gather: an unroll of 8 (512 lanes per span, 4 loads
+// each; 106 SGPRs, one workgroup per CU: 5.1 against 5.9 TB/s), and
+// global-address-space loads and stores in place of the flat ones the table
+// addresses compile to (equal on 32 KiB spans, 5.6 against 5.9 TB/s on 64 KiB
+// ones).
 constexpr int kGatherThreads = 1024, kGatherUnroll = 4;
 // Scatter from device records: HBM to HBM like the gather, writes scattered.
 constexpr int kScatterThreads = 1024, kScatterUnroll = 4;
@@ -185,6 +187,63 @@ __global__ __launch_bounds__(kScatterThreads) void scatter_kernel(
         char* dst = reinterpret_cast<char*>(bases[s] + blocks[b] * pitches[s]);
         copy_span<kScatterUnroll>(src, dst, words[s] * 8, jl.lane, jl.lanes);
     }
+}
+
+// Gather and scatter in pieces: one wave per KiB of a span, one 16-byte load
+// and one store per lane.  Workgroup x copies piece x % pieces of job
+// x / pieces (jobs in the order above).  A span's last piece takes every byte
+// from its KiB to the span's end, so `pieces` (the host's ceil(shortest span
+// / 1 KiB)) shapes the launch without changing what is copied: a longer
+// span's last wave loops over the rest, and a piece past a span's end copies
+// nothing.  On the 8k Qwen3-8B gather (36,864 spans of 32 KiB) this shape ran
+// at 6.5 TB/s, against 5.7-5.8 for one 1024-lane workgroup per span
+// (gather_kernel above) and 6.2 for 256-lane workgroups per 4 KiB piece.
+// Each wave lives for one load and one store, and the dispatcher keeps the
+// CUs full of them.  Pieces dealt to the XCDs in contiguous ranges ran at
+// 6.35 TB/s, so consecutive pieces go round robin.
+constexpr int kPieceBytes = 64 * 16;
+
+template <bool kGather>
+__device__ __forceinline__ void copy_piece(const int64_t* __restrict__ blocks, const int64_t* __restrict__ offs,
+                                           const int64_t* __restrict__ bases, const int64_t* __restrict__ pitches,
+                                           const int64_t* __restrict__ words, uint32_t n_spans, uint32_t pieces,
+                                           char* __restrict__ records, int64_t record_pitch) {
+    const uint32_t x = blockIdx.x;
+    const uint32_t job = x / pieces, p = x - job * pieces;
+    const uint32_t b = job / n_spans, s = job - b * n_spans;
+    const int64_t length = words[s] * 8, at = static_cast<int64_t>(p) * kPieceBytes;
+    if (at >= length) return;
+    const int64_t end = p + 1 == pieces || length - at < kPieceBytes ? length : at + kPieceBytes;
+    char* cache = reinterpret_cast<char*>(bases[s] + blocks[b] * pitches[s]) + at;
+    char* record = records + static_cast<int64_t>(b) * record_pitch + offs[s] + at;
+    const char* src = kGather ? cache : record;
+    char* dst = kGather ? record : cache;
+    const int lane = static_cast<int>(threadIdx.x);
+    if (end - at == kPieceBytes && ((reinterpret_cast<uintptr_t>(src) | reinterpret_cast<uintptr_t>(dst)) & 15) == 0)
+        __builtin_nontemporal_store(__builtin_nontemporal_load(reinterpret_cast<const u32x4*>(src) + lane),
+                                    reinterpret_cast<u32x4*>(dst) + lane);
+    else
+        copy_span<1>(src, dst, end - at, lane, 64);
+}
+
+__global__ __launch_bounds__(64) void gather_pieces_kernel(const int64_t* __restrict__ blocks,
+                                                           const int64_t* __restrict__ offs,
+                                                           const int64_t* __restrict__ bases,
+                                                           const int64_t* __restrict__ pitches,
+                                                           const int64_t* __restrict__ words, uint32_t n_spans,
+                                                           uint32_t pieces, char* __restrict__ records,
+                                                           int64_t record_pitch) {
+    copy_piece<true>(blocks, offs, bases, pitches, words, n_spans, pieces, records, record_pitch);
+}
+
+__global__ __launch_bounds__(64) void scatter_pieces_kernel(const int64_t* __restrict__ blocks,
+                                                            const int64_t* __restrict__ offs,
+                                                            const int64_t* __restrict__ bases,
+                                                            const int64_t* __restrict__ pitches,
+                                                            const int64_t* __restrict__ words, uint32_t n_spans,
+                                                            uint32_t pieces, char* __restrict__ records,
+                                                            int64_t record_pitch) {
+    copy_piece<false>(blocks, offs, bases, pitches, words, n_spans, pieces, records, record_pitch);
 }
 
 // Gather into per-block destinations (pinned host records written in place
@@ -1644,6 +1703,37 @@ CopyShape copy_shape(int threads, int unroll, int64_t jobs, int64_t min_span_byt
     return CopyShape{shift, grid_for((jobs + per_pass - 1) / per_pass, programs)};
 }
 
+// The pieces kernels' launches: ceil(shortest span / 1 KiB) pieces per span
+// (at most kMaxPieces; a longer span's last wave loops over the rest), and as
+// many launches as the blocks need for each grid to stay under 2^32 lanes.
+constexpr int64_t kMaxPieces = 1024;
+constexpr int64_t kMaxPieceWorkgroups = int64_t(1) << 25;
+
+int64_t span_pieces(int64_t min_span_bytes) {
+    const int64_t pieces = (min_span_bytes + kPieceBytes - 1) / kPieceBytes;
+    return pieces < 1 ? 1 : pieces > kMaxPieces ? kMaxPieces : pieces;
+}
+
+// Whether a copy launch goes by pieces: a grid sized to the work (programs <= 0) and a known span length.
+bool by_pieces(int64_t n_spans, int64_t min_span_bytes, int programs) {
+    return programs <= 0 && min_span_bytes > 0 && n_spans * span_pieces(min_span_bytes) <= kMaxPieceWorkgroups;
+}
+
+template <bool kGather>
+void launch_pieces(const int64_t* blocks, int64_t n_blocks, const int64_t* offs, const int64_t* bases,
+                   const int64_t* pitches, const int64_t* words, int64_t n_spans, int64_t min_span_bytes,
+                   char* records, int64_t record_pitch, hipStream_t stream) {
+    const int64_t pieces = span_pieces(min_span_bytes), per_block = n_spans * pieces;
+    const int64_t blocks_per_launch = kMaxPieceWorkgroups / per_block;
+    for (int64_t first = 0; first < n_blocks; first += blocks_per_launch) {
+        const int64_t count = n_blocks - first < blocks_per_launch ? n_blocks - first : blocks_per_launch;
+        hipLaunchKernelGGL(kGather ? gather_pieces_kernel : scatter_pieces_kernel, dim3(static_cast<unsigned>(count * per_block)), dim3(64), 0,
+                           stream, blocks + first, offs, bases, pitches, words, static_cast<uint32_t>(n_spans),
+                           static_cast<uint32_t>(pieces), records + first * record_pitch, record_pitch);
+        check_launch(kGather ? "gather" : "scatter");
+    }
+}
+
 struct CrcPlan {
     int groups;       // 4 KiB groups per stripe (one wave's job)
     int64_t stripes;  // per record, at most kCrcMaxStripes
@@ -1837,6 +1927,12 @@ int kvsnap_scatter_blocks(const void* records, int64_t record_pitch, const int64
         if (n_blocks == 0 || n_spans == 0) return;
         if (!records || !blocks || !span_offsets || !span_bases || !span_pitches || !span_words)
             throw std::runtime_error("scatter tables must be device pointers");
+        if (by_pieces(n_spans, min_span_bytes, programs)) {
+            launch_pieces<false>(blocks, n_blocks, span_offsets, span_bases, span_pitches, span_words, n_spans,
+                                 min_span_bytes, const_cast<char*>(static_cast<const char*>(records)), record_pitch,
+                                 reinterpret_cast<hipStream_t>(stream));
+            return;
+        }
         const CopyShape shape = copy_shape(kScatterThreads, kScatterUnroll, n_blocks * n_spans, min_span_bytes,
                                            programs);
         hipLaunchKernelGGL(scatter_kernel, dim3(shape.grid), dim3(kScatterThreads), 0,
@@ -1856,6 +1952,12 @@ int kvsnap_gather_blocks(const int64_t* blocks, int64_t n_blocks, const int64_t*
         if (n_blocks == 0 || n_spans == 0) return;
         if (!records || !blocks || !span_offsets || !span_bases || !span_pitches || !span_words)
             throw std::runtime_error("gather tables must be device pointers");
+        if (by_pieces(n_spans, min_span_bytes, programs)) {
+            launch_pieces<true>(blocks, n_blocks, span_offsets, span_bases, span_pitches, span_words, n_spans,
+                                min_span_bytes, static_cast<char*>(records), record_pitch,
+                                reinterpret_cast<hipStream_t>(stream));
+            return;
+        }
         const CopyShape shape = copy_shape(kGatherThreads, kGatherUnroll, n_blocks * n_spans, min_span_bytes,
                                            programs);
         hipLaunchKernelGGL(gather_kernel, dim3(shape.grid), dim3(kGatherThreads), 0,
