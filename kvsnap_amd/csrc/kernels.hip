@@ -190,12 +190,12 @@ __global__ __launch_bounds__(kScatterThreads) void scatter_kernel(
 }
 
 // Gather and scatter in pieces: one wave per KiB of a span, one 16-byte load
-// and one store per lane.  Workgroup x copies piece x % pieces of job
-// x / pieces (jobs in the order above).  A span's last piece takes every byte
-// from its KiB to the span's end, so `pieces` (the host's ceil(shortest span
-// / 1 KiB)) shapes the launch without changing what is copied: a longer
-// span's last wave loops over the rest, and a piece past a span's end copies
-// nothing.  On the 8k Qwen3-8B gather (36,864 spans of 32 KiB) this shape ran
+// and one store per lane.  Workgroup (x, b) copies piece x % pieces of span
+// x / pieces of block b (dispatched x first, so in the jobs' order above).  A
+// span's last piece takes every byte from its KiB to the span's end, so
+// `pieces` (the host's ceil(shortest span / 1 KiB)) shapes the launch without
+// changing what is copied: a longer span's last wave loops over the rest,
+// and a piece past a span's end copies nothing.  On the 8k Qwen3-8B gather (36,864 spans of 32 KiB) this shape ran
 // at 6.5 TB/s, against 5.7-5.8 for one 1024-lane workgroup per span
 // (gather_kernel above) and 6.2 for 256-lane workgroups per 4 KiB piece.
 // Each wave lives for one load and one store, and the dispatcher keeps the
@@ -206,11 +206,9 @@ constexpr int kPieceBytes = 64 * 16;
 template <bool kGather>
 __device__ __forceinline__ void copy_piece(const int64_t* __restrict__ blocks, const int64_t* __restrict__ offs,
                                            const int64_t* __restrict__ bases, const int64_t* __restrict__ pitches,
-                                           const int64_t* __restrict__ words, uint32_t n_spans, uint32_t pieces,
+                                           const int64_t* __restrict__ words, uint32_t pieces,
                                            char* __restrict__ records, int64_t record_pitch) {
-    const uint32_t x = blockIdx.x;
-    const uint32_t job = x / pieces, p = x - job * pieces;
-    const uint32_t b = job / n_spans, s = job - b * n_spans;
+    const uint32_t b = blockIdx.y, s = blockIdx.x / pieces, p = blockIdx.x - s * pieces;
     const int64_t length = words[s] * 8, at = static_cast<int64_t>(p) * kPieceBytes;
     if (at >= length) return;
     const int64_t end = p + 1 == pieces || length - at < kPieceBytes ? length : at + kPieceBytes;
@@ -230,20 +228,18 @@ __global__ __launch_bounds__(64) void gather_pieces_kernel(const int64_t* __rest
                                                            const int64_t* __restrict__ offs,
                                                            const int64_t* __restrict__ bases,
                                                            const int64_t* __restrict__ pitches,
-                                                           const int64_t* __restrict__ words, uint32_t n_spans,
-                                                           uint32_t pieces, char* __restrict__ records,
-                                                           int64_t record_pitch) {
-    copy_piece<true>(blocks, offs, bases, pitches, words, n_spans, pieces, records, record_pitch);
+                                                           const int64_t* __restrict__ words, uint32_t pieces,
+                                                           char* __restrict__ records, int64_t record_pitch) {
+    copy_piece<true>(blocks, offs, bases, pitches, words, pieces, records, record_pitch);
 }
 
 __global__ __launch_bounds__(64) void scatter_pieces_kernel(const int64_t* __restrict__ blocks,
                                                             const int64_t* __restrict__ offs,
                                                             const int64_t* __restrict__ bases,
                                                             const int64_t* __restrict__ pitches,
-                                                            const int64_t* __restrict__ words, uint32_t n_spans,
-                                                            uint32_t pieces, char* __restrict__ records,
-                                                            int64_t record_pitch) {
-    copy_piece<false>(blocks, offs, bases, pitches, words, n_spans, pieces, records, record_pitch);
+                                                            const int64_t* __restrict__ words, uint32_t pieces,
+                                                            char* __restrict__ records, int64_t record_pitch) {
+    copy_piece<false>(blocks, offs, bases, pitches, words, pieces, records, record_pitch);
 }
 
 // Gather into per-block destinations (pinned host records written in place
@@ -1703,9 +1699,9 @@ CopyShape copy_shape(int threads, int unroll, int64_t jobs, int64_t min_span_byt
     return CopyShape{shift, grid_for((jobs + per_pass - 1) / per_pass, programs)};
 }
 
-// The pieces kernels' launches: ceil(shortest span / 1 KiB) pieces per span
-// (at most kMaxPieces; a longer span's last wave loops over the rest), and as
-// many launches as the blocks need for each grid to stay under 2^32 lanes.
+// The pieces kernels' grid: ceil(shortest span / 1 KiB) pieces per span (at
+// most kMaxPieces; a longer span's last wave loops over the rest) times the
+// spans in x, the blocks in y, each dimension under 2^32 lanes.
 constexpr int64_t kMaxPieces = 1024;
 constexpr int64_t kMaxPieceWorkgroups = int64_t(1) << 25;
 
@@ -1714,24 +1710,22 @@ int64_t span_pieces(int64_t min_span_bytes) {
     return pieces < 1 ? 1 : pieces > kMaxPieces ? kMaxPieces : pieces;
 }
 
-// Whether a copy launch goes by pieces: a grid sized to the work (programs <= 0) and a known span length.
-bool by_pieces(int64_t n_spans, int64_t min_span_bytes, int programs) {
-    return programs <= 0 && min_span_bytes > 0 && n_spans * span_pieces(min_span_bytes) <= kMaxPieceWorkgroups;
+// Whether a copy launch goes by pieces: a grid sized to the work (programs <= 0), a known span length and
+// both grid dimensions in range.
+bool by_pieces(int64_t n_blocks, int64_t n_spans, int64_t min_span_bytes, int programs) {
+    return programs <= 0 && min_span_bytes > 0 && n_spans * span_pieces(min_span_bytes) <= kMaxPieceWorkgroups &&
+           n_blocks <= kMaxPieceWorkgroups;
 }
 
 template <bool kGather>
 void launch_pieces(const int64_t* blocks, int64_t n_blocks, const int64_t* offs, const int64_t* bases,
                    const int64_t* pitches, const int64_t* words, int64_t n_spans, int64_t min_span_bytes,
                    char* records, int64_t record_pitch, hipStream_t stream) {
-    const int64_t pieces = span_pieces(min_span_bytes), per_block = n_spans * pieces;
-    const int64_t blocks_per_launch = kMaxPieceWorkgroups / per_block;
-    for (int64_t first = 0; first < n_blocks; first += blocks_per_launch) {
-        const int64_t count = n_blocks - first < blocks_per_launch ? n_blocks - first : blocks_per_launch;
-        hipLaunchKernelGGL(kGather ? gather_pieces_kernel : scatter_pieces_kernel, dim3(static_cast<unsigned>(count * per_block)), dim3(64), 0,
-                           stream, blocks + first, offs, bases, pitches, words, static_cast<uint32_t>(n_spans),
-                           static_cast<uint32_t>(pieces), records + first * record_pitch, record_pitch);
-        check_launch(kGather ? "gather" : "scatter");
-    }
+    const int64_t pieces = span_pieces(min_span_bytes);
+    const dim3 grid(static_cast<unsigned>(n_spans * pieces), static_cast<unsigned>(n_blocks));
+    hipLaunchKernelGGL(kGather ? gather_pieces_kernel : scatter_pieces_kernel, grid, dim3(64), 0, stream, blocks,
+                       offs, bases, pitches, words, static_cast<uint32_t>(pieces), records, record_pitch);
+    check_launch(kGather ? "gather" : "scatter");
 }
 
 struct CrcPlan {
@@ -1927,7 +1921,7 @@ int kvsnap_scatter_blocks(const void* records, int64_t record_pitch, const int64
         if (n_blocks == 0 || n_spans == 0) return;
         if (!records || !blocks || !span_offsets || !span_bases || !span_pitches || !span_words)
             throw std::runtime_error("scatter tables must be device pointers");
-        if (by_pieces(n_spans, min_span_bytes, programs)) {
+        if (by_pieces(n_blocks, n_spans, min_span_bytes, programs)) {
             launch_pieces<false>(blocks, n_blocks, span_offsets, span_bases, span_pitches, span_words, n_spans,
                                  min_span_bytes, const_cast<char*>(static_cast<const char*>(records)), record_pitch,
                                  reinterpret_cast<hipStream_t>(stream));
@@ -1952,7 +1946,7 @@ int kvsnap_gather_blocks(const int64_t* blocks, int64_t n_blocks, const int64_t*
         if (n_blocks == 0 || n_spans == 0) return;
         if (!records || !blocks || !span_offsets || !span_bases || !span_pitches || !span_words)
             throw std::runtime_error("gather tables must be device pointers");
-        if (by_pieces(n_spans, min_span_bytes, programs)) {
+        if (by_pieces(n_blocks, n_spans, min_span_bytes, programs)) {
             launch_pieces<true>(blocks, n_blocks, span_offsets, span_bases, span_pitches, span_words, n_spans,
                                 min_span_bytes, static_cast<char*>(records), record_pitch,
                                 reinterpret_cast<hipStream_t>(stream));
