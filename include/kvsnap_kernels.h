@@ -16,10 +16,12 @@
  * layer (K, then V) for [2, blocks, N, H, C] caches.
  *
  * Copy launches take `min_span_bytes`, the length of the shortest span (0 if
- * unknown): a launch-shape hint that never changes what is copied.  Short
- * spans (a tensor-parallel rank's shard, fp8 caches) are then copied several
- * to a workgroup.  `programs` caps the grid (<= 0: as many workgroups as the
- * jobs need).
+ * unknown): a launch-shape hint that never changes what is copied.
+ * `programs` caps the grid (<= 0: as many workgroups as the work needs).  A
+ * gather or scatter with programs <= 0 and a known hint goes one 64-lane
+ * workgroup per KiB of a span; otherwise a workgroup takes (block, span)
+ * jobs in turn, and short spans (a tensor-parallel rank's shard, fp8 caches)
+ * are copied several to a workgroup.
  */
 #ifndef KVSNAP_KERNELS_H
 #define KVSNAP_KERNELS_H
