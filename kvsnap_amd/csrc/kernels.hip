@@ -1701,9 +1701,11 @@ CopyShape copy_shape(int threads, int unroll, int64_t jobs, int64_t min_span_byt
 
 // The pieces kernels' grid: ceil(shortest span / 1 KiB) pieces per span (at
 // most kMaxPieces; a longer span's last wave loops over the rest) times the
-// spans in x, the blocks in y, each dimension under 2^32 lanes.
+// spans in x, the blocks in y, at most kMaxPieceBlocks blocks a launch (the
+// grid's y limit HIP states for every device).
 constexpr int64_t kMaxPieces = 1024;
 constexpr int64_t kMaxPieceWorkgroups = int64_t(1) << 25;
+constexpr int64_t kMaxPieceBlocks = 65535;
 
 int64_t span_pieces(int64_t min_span_bytes) {
     const int64_t pieces = (min_span_bytes + kPieceBytes - 1) / kPieceBytes;
@@ -1711,10 +1713,9 @@ int64_t span_pieces(int64_t min_span_bytes) {
 }
 
 // Whether a copy launch goes by pieces: a grid sized to the work (programs <= 0), a known span length and
-// both grid dimensions in range.
-bool by_pieces(int64_t n_blocks, int64_t n_spans, int64_t min_span_bytes, int programs) {
-    return programs <= 0 && min_span_bytes > 0 && n_spans * span_pieces(min_span_bytes) <= kMaxPieceWorkgroups &&
-           n_blocks <= kMaxPieceWorkgroups;
+// a grid x dimension in range.
+bool by_pieces(int64_t n_spans, int64_t min_span_bytes, int programs) {
+    return programs <= 0 && min_span_bytes > 0 && n_spans * span_pieces(min_span_bytes) <= kMaxPieceWorkgroups;
 }
 
 template <bool kGather>
@@ -1722,10 +1723,14 @@ void launch_pieces(const int64_t* blocks, int64_t n_blocks, const int64_t* offs,
                    const int64_t* pitches, const int64_t* words, int64_t n_spans, int64_t min_span_bytes,
                    char* records, int64_t record_pitch, hipStream_t stream) {
     const int64_t pieces = span_pieces(min_span_bytes);
-    const dim3 grid(static_cast<unsigned>(n_spans * pieces), static_cast<unsigned>(n_blocks));
-    hipLaunchKernelGGL(kGather ? gather_pieces_kernel : scatter_pieces_kernel, grid, dim3(64), 0, stream, blocks,
-                       offs, bases, pitches, words, static_cast<uint32_t>(pieces), records, record_pitch);
-    check_launch(kGather ? "gather" : "scatter");
+    for (int64_t first = 0; first < n_blocks; first += kMaxPieceBlocks) {
+        const int64_t count = n_blocks - first < kMaxPieceBlocks ? n_blocks - first : kMaxPieceBlocks;
+        const dim3 grid(static_cast<unsigned>(n_spans * pieces), static_cast<unsigned>(count));
+        hipLaunchKernelGGL(kGather ? gather_pieces_kernel : scatter_pieces_kernel, grid, dim3(64), 0, stream,
+                           blocks + first, offs, bases, pitches, words, static_cast<uint32_t>(pieces),
+                           records + first * record_pitch, record_pitch);
+        check_launch(kGather ? "gather" : "scatter");
+    }
 }
 
 struct CrcPlan {
@@ -1921,7 +1926,7 @@ int kvsnap_scatter_blocks(const void* records, int64_t record_pitch, const int64
         if (n_blocks == 0 || n_spans == 0) return;
         if (!records || !blocks || !span_offsets || !span_bases || !span_pitches || !span_words)
             throw std::runtime_error("scatter tables must be device pointers");
-        if (by_pieces(n_blocks, n_spans, min_span_bytes, programs)) {
+        if (by_pieces(n_spans, min_span_bytes, programs)) {
             launch_pieces<false>(blocks, n_blocks, span_offsets, span_bases, span_pitches, span_words, n_spans,
                                  min_span_bytes, const_cast<char*>(static_cast<const char*>(records)), record_pitch,
                                  reinterpret_cast<hipStream_t>(stream));
@@ -1946,7 +1951,7 @@ int kvsnap_gather_blocks(const int64_t* blocks, int64_t n_blocks, const int64_t*
         if (n_blocks == 0 || n_spans == 0) return;
         if (!records || !blocks || !span_offsets || !span_bases || !span_pitches || !span_words)
             throw std::runtime_error("gather tables must be device pointers");
-        if (by_pieces(n_blocks, n_spans, min_span_bytes, programs)) {
+        if (by_pieces(n_spans, min_span_bytes, programs)) {
             launch_pieces<true>(blocks, n_blocks, span_offsets, span_bases, span_pitches, span_words, n_spans,
                                 min_span_bytes, static_cast<char*>(records), record_pitch,
                                 reinterpret_cast<hipStream_t>(stream));
