@@ -349,6 +349,7 @@ def run_save_restore(args):
         t3 = time.perf_counter()
         plane.load_scatter_checked(target, targets, saved_crcs)
         t4 = time.perf_counter()
+        lat_timer.reset()
         plane.timer = lat_timer if i else None
         plane.load_scatter(target, targets, progress=progress)
         t5 = time.perf_counter()
@@ -364,10 +365,12 @@ def run_save_restore(args):
             latency["hashed"].append((t2 - t0) * 1e3)
             latency["restore"].append((t3 - t2) * 1e3)
             latency["timed_restore"].append((t5 - t4) * 1e3)
-            launches = len(progress) - 1
-            pairs = lat_timer.pairs["restore"][-launches:]
-            latency["early"].append(pairs[0][0].elapsed_time(pairs[early_launch_index(progress)][1]))
-            latency["timed_restore_gpu_span"].append(pairs[0][0].elapsed_time(pairs[-1][1]))
+            # Per launch: the restore kernel's spans, or with copy-engine restores the placements' (the copies
+            # are timed per copy, up to four launches' blocks at a time); the span opens at the first copy.
+            pairs = lat_timer.pairs["restore" if plane.restore_mode == "kernel" else "place"]
+            start = lat_timer.pairs["restore"][0][0]
+            latency["early"].append(start.elapsed_time(pairs[early_launch_index(progress)][1]))
+            latency["timed_restore_gpu_span"].append(start.elapsed_time(pairs[-1][1]))
             latency["timed_restore_longest_launch"].append(max(a.elapsed_time(b) for a, b in pairs))
     lat = {k: statistics.median(v) for k, v in latency.items()}
     checked_launch_ms = lat_timer.summary()["restore_checked"]["avg_ms"]
@@ -416,7 +419,7 @@ def run_save_restore(args):
     drain()
     plane.timer = None
     kernels = dict(in_step.summary(), gather=timer.summary()["gather"])
-    launches = kernels["restore"]["launches"] // instrumented_steps
+    launches = len(plane._launch_bounds(session, 64 << 20))     # a restore's launches at the default chunking
 
     # Parity of the last step, outside the timed region.
     import oracle
