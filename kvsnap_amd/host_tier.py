@@ -210,7 +210,7 @@ class HostTier:
         return dict(block_ids=block_ids, num_kv_tokens=num_kv_tokens, segments=segments,
                     locations=self.locations(segments), kv_layout=plane.layout_identity)
 
-    def restore(self, block_ids, snapshot, *, verify=False, progress=None, chunk_bytes=64 << 20):
+    def restore(self, block_ids, snapshot, *, verify=False, progress=None, chunk_bytes=None):
         """Scatter a held snapshot into ``block_ids``; returns the snapshot as restored there.
 
         Every block is checked as held before any copy, and the blocks stay
