@@ -159,17 +159,17 @@ def cpu_baseline(layers, span, records=512, seconds_per_leg=0.6):
       at ``store.py:621-622``, ``volatile.py:229-232``);
     * pread: the records read back from a page-cached file into host memory
       by reader threads, each taking one record at a time and checking its
-      CRC32C (``read_prepared_into``, ``store.py:686-723``), through the
-      reference's own compiled ``io.cpp`` pool when ``oracle/_ref`` holds it.
+      CRC32C (``read_prepared_into``, ``store.py:686-723``), through this
+      repository's ``io.cpp`` pool (the reference's I/O C-ABI).
 
     Each leg runs on 1 thread, on 8 (the reference's hash and read pools) and
     on the host's share ``N`` (``host_threads``).  ``value``: save + restore
     bytes over gather + CRC32C + SHA-256 + scatter at ``N`` threads.
     """
     import concurrent.futures
-    import ctypes as C
     import numpy as np
     import oracle
+    from kvsnap_amd.native_io import IO_LIBRARY, NativeIO
     oracle.build()
     oracle.sha256_select(True)
     lib = oracle.lib()
@@ -210,16 +210,6 @@ def cpu_baseline(layers, span, records=512, seconds_per_leg=0.6):
     gather(widest)
     crc(widest)
     expected = crcs.copy()
-    ref_path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "oracle", "_ref", "libkvsnap_io_ref.so")
-    ref = C.CDLL(ref_path) if os.path.isfile(ref_path) else None
-    if ref is not None:
-        ref.kvsnap_io_pool_create.argtypes, ref.kvsnap_io_pool_create.restype = [C.c_size_t, C.c_size_t], C.c_void_p
-        ref.kvsnap_io_pool_destroy.argtypes, ref.kvsnap_io_pool_destroy.restype = [C.c_void_p], None
-        ref.kvsnap_io_pool_transfer.argtypes = [C.c_void_p, C.c_int, C.c_void_p, C.c_size_t, C.c_int64, C.c_int,
-                                                C.c_int]
-        ref.kvsnap_io_pool_transfer.restype = C.c_int
-        ref.kvsnap_crc32c_extend.argtypes = [C.c_void_p, C.c_size_t, C.c_uint32]
-        ref.kvsnap_crc32c_extend.restype = C.c_uint32
     legs = {"gather": gather, "scatter": scatter, "crc32c": crc, "sha256": sha}
     thread_counts = sorted({1, 8, widest})
     result = {name: {} for name in list(legs) + ["pread"]}
@@ -230,28 +220,21 @@ def cpu_baseline(layers, span, records=512, seconds_per_leg=0.6):
         fd = os.open(path, os.O_RDONLY)
         try:
             def pread(threads):
-                pool = ref.kvsnap_io_pool_create(threads, 64 << 20) if ref is not None else None
+                # The reference's read path (store.py:686-723): reader threads each pread one record through a
+                # native I/O pool of as many workers (this repository's io.cpp, the same C-ABI) and check its
+                # CRC32C (the oracle's SSE4.2 restatement of io.cpp:16-47).
+                io = NativeIO(IO_LIBRARY, workers=threads, queue_bytes=64 << 20)
 
                 def one(i):
                     at = packed.ctypes.data + i * record
-                    if pool is not None:
-                        code = ref.kvsnap_io_pool_transfer(pool, fd, at, record, i * record, 0, 0)
-                        if code:
-                            raise OSError(code, os.strerror(code))
-                        found = ref.kvsnap_crc32c_extend(at, record, 0)
-                    else:
-                        view = memoryview(packed)[i * record:(i + 1) * record]
-                        if os.preadv(fd, [view], i * record) != record:
-                            raise OSError("short read")
-                        found = oracle.crc32c_at(at, record)
-                    if found != expected[i]:
+                    io.pread_into(fd, at, record, i * record)
+                    if oracle.crc32c_at(at, record) != expected[i]:
                         raise RuntimeError("a record read back fails its CRC32C")
                 try:
                     with concurrent.futures.ThreadPoolExecutor(threads) as readers:
                         list(readers.map(one, range(records)))
                 finally:
-                    if pool is not None:
-                        ref.kvsnap_io_pool_destroy(pool)
+                    io.close()
 
             legs["pread"] = pread
             for threads in thread_counts:
@@ -269,7 +252,7 @@ def cpu_baseline(layers, span, records=512, seconds_per_leg=0.6):
                           for name, times in result.items()},
             "legs_ms": {name: {str(t): round(s * 1e3, 2) for t, s in times.items()} for name, times in result.items()},
             "save_restore_gbps": {str(t): round(v, 3) for t, v in save_restore.items()},
-            "pread_kind": "reference (oracle/_ref io.cpp pool)" if ref is not None else "port (os.preadv)",
+            "pread_kind": "this repository's io.cpp pool (threads workers) + the oracle's CRC32C",
             "sample": (f"the {records}-record snapshot ({records} x {record} B = {total} B) gathered from and "
                        f"scattered into a {host_blocks}-block host cache; best of repeated runs per leg; pread from "
                        f"a page-cached file"),

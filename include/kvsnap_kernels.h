@@ -36,6 +36,14 @@ extern "C" {
 /* Always 2 (2 added min_span_bytes to the copy launches). */
 int kvsnap_kernels_abi_version(void);
 
+/* Set-up for `device`, synchronous: uploads the CRC32C tables and looks up the
+ * no-allocation entry point's static array on that device (the current device
+ * is restored on return).  Idempotent.  The other entry points set up a
+ * device on their first call there; kvsnap_crc32c_records_noalloc refuses a
+ * device that this call has not set up.  No counterpart in the reference
+ * (its copy kernel needs no tables); TorchBlockDataPlane.warm_up calls it. */
+int kvsnap_kernels_init(int device);
+
 /* Restore: for every (block i, span s), copy span_words[s] words from
  * sources[i] + span_offsets[s] to span_bases[s] + blocks[i] * span_pitches[s].
  * Replaces the Triton launch copy_host_blocks(sources, blocks,
@@ -138,8 +146,9 @@ int kvsnap_crc32c_records(const void* records, uint64_t record_bytes, uint64_t r
  * batch fails with an error before anything is queued).  Calls that overlap
  * on one GPU race on that array, so callers order them (one stream, or
  * events).  The array keeps the last call's partials; a call reads only what
- * it has written.  The first call on a device uploads the CRC tables and
- * looks up the array's address (synchronous), so make one before capturing. */
+ * it has written.  Call kvsnap_kernels_init(device) once first (it uploads
+ * the tables and finds the array, synchronously): this entry point makes no
+ * synchronous call, and refuses a device that was not set up. */
 int kvsnap_crc32c_records_noalloc(const void* records, uint64_t record_bytes, uint64_t record_pitch,
                                   int64_t n_records, uint32_t prior, uint32_t* out, uintptr_t stream);
 

@@ -1831,18 +1831,26 @@ constexpr int64_t kStaticCrcMaxRecords = kStaticCrcPartials;
 __device__ __align__(256) uint32_t scratch[kStaticCrcPartials];
 uint32_t* g_scratch_ptr[64];
 
+// With `device` current: look up the array's address on it, once.
+void init_static_crc_workspace(int device) {
+    std::lock_guard<std::mutex> lock(g_table_mutex);
+    if (g_scratch_ptr[device]) return;
+    void* ptr = nullptr;
+    const hipError_t rc = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (rc != hipSuccess || !ptr)
+        throw std::runtime_error(std::string("CRC32C static workspace address: ") + hipGetErrorString(rc));
+    g_scratch_ptr[device] = static_cast<uint32_t*>(ptr);
+}
+
+// The current device's array and tables, set up by kvsnap_kernels_init: the
+// no-allocation entry point makes no synchronous call of its own.
 uint32_t* static_crc_workspace() {
     int device = 0;
     if (hipGetDevice(&device) != hipSuccess || device < 0 || device >= 64)
         throw std::runtime_error("no current HIP device for the CRC32C workspace");
     std::lock_guard<std::mutex> lock(g_table_mutex);
-    if (!g_scratch_ptr[device]) {
-        void* ptr = nullptr;
-        const hipError_t rc = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
-        if (rc != hipSuccess || !ptr)
-            throw std::runtime_error(std::string("CRC32C static workspace address: ") + hipGetErrorString(rc));
-        g_scratch_ptr[device] = static_cast<uint32_t*>(ptr);
-    }
+    if (!g_scratch_ptr[device] || !g_tables_ready[device])
+        throw std::runtime_error("CRC32C without allocation: call kvsnap_kernels_init for this device first");
     return g_scratch_ptr[device];
 }
 
@@ -1860,6 +1868,26 @@ static_assert(kCopyLdsFence + sizeof(ShaSchedule) > 160 * 1024, "a copy and a SH
 extern "C" {
 
 int kvsnap_kernels_abi_version() { return 2; }
+
+int kvsnap_kernels_init(int device) {
+    return guard([&] {
+        if (device < 0 || device >= 64) throw std::runtime_error("device index out of range");
+        int previous = 0;
+        hipError_t rc = hipGetDevice(&previous);
+        if (rc != hipSuccess) throw std::runtime_error(std::string("hipGetDevice: ") + hipGetErrorString(rc));
+        rc = hipSetDevice(device);
+        if (rc != hipSuccess) throw std::runtime_error(std::string("hipSetDevice: ") + hipGetErrorString(rc));
+        try {
+            ensure_crc_tables();
+            init_static_crc_workspace(device);
+        } catch (...) {
+            (void)hipSetDevice(previous);
+            throw;
+        }
+        rc = hipSetDevice(previous);
+        if (rc != hipSuccess) throw std::runtime_error(std::string("hipSetDevice: ") + hipGetErrorString(rc));
+    });
+}
 
 int kvsnap_restore_blocks(const int64_t* sources, const int64_t* blocks, int64_t n_blocks,
                           const int64_t* span_offsets, const int64_t* span_bases, const int64_t* span_pitches,
@@ -2077,8 +2105,8 @@ int kvsnap_crc32c_records_noalloc(const void* records, uint64_t record_bytes, ui
         const CrcPlan plan = crc_plan(record_bytes, n_records, kStaticCrcPartials);
         if (plan.stripes * n_records > kStaticCrcPartials)
             throw std::runtime_error("CRC32C without allocation: the static workspace is too small");
-        ensure_crc_tables();
-        launch_crc32c(records, record_bytes, record_pitch, n_records, prior, out, static_crc_workspace(), plan,
+        uint32_t* partials = static_crc_workspace();    // refuses a device kvsnap_kernels_init has not set up
+        launch_crc32c(records, record_bytes, record_pitch, n_records, prior, out, partials, plan,
                       reinterpret_cast<hipStream_t>(stream));
     });
 }

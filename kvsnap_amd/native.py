@@ -41,6 +41,7 @@ def resolve_cuda_library(library=None):
 KERNEL_SIGNATURES = {
     "kvsnap_cuda_error": "str <-",
     "kvsnap_kernels_abi_version": "int <-",
+    "kvsnap_kernels_init": "int <- int",
     "kvsnap_restore_blocks": "int <- ptr ptr i64 ptr ptr ptr ptr i64 i64 int stream",
     "kvsnap_restore_blocks_checked": "int <- ptr ptr i64 ptr ptr ptr ptr i64 int ptr stream",
     "kvsnap_restore_checked_crc32c": "int <- ptr i64 ptr ptr i64 u64 ptr stream",

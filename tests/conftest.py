@@ -44,3 +44,22 @@ def oracle_lib():
     import oracle
     oracle.build()
     return oracle
+
+
+@pytest.fixture
+def planes(hip_library):
+    """A maker of warmed-up data planes (block size 16 unless asked), each closed when the test ends."""
+    import torch
+    from kvsnap_amd.dataplane import TorchBlockDataPlane
+    made = []
+
+    def make(caches, block_size=16, capacity=64 << 20, **kwargs):
+        plane = TorchBlockDataPlane(caches, block_size, capacity, **kwargs)
+        plane.warm_up()
+        made.append(plane)
+        return plane
+
+    yield make
+    torch.cuda.synchronize()
+    for plane in made:
+        plane.close()

@@ -21,22 +21,6 @@ pytestmark = pytest.mark.gpu
 LAYERS, BLOCKS, BLOCK_SIZE, HEADS, WIDTH = 6, 96, 16, 8, 256
 
 
-@pytest.fixture
-def planes(hip_library):
-    made = []
-
-    def make(caches, block_size=BLOCK_SIZE, capacity=64 << 20, **kwargs):
-        plane = TorchBlockDataPlane(caches, block_size, capacity, **kwargs)
-        plane.warm_up()
-        made.append(plane)
-        return plane
-
-    yield make
-    torch.cuda.synchronize()
-    for plane in made:
-        plane.close()
-
-
 def vllm_caches(layers, blocks, seed=0):
     """The reference's GPU fixture: random bf16 bits, [blocks, H, N, 2D] views of [blocks, N, H, 2D] storage."""
     generator = torch.Generator(device="cuda").manual_seed(seed)
@@ -728,8 +712,12 @@ def test_qwen3_1_7b_round_trip_at_the_cpu_reference_shape(planes, oracle_lib):
 
 def test_qwen3_8b_8k_session_at_full_size(planes, oracle_lib):
     """The headline workload's shape: 36 K/V-split layers in a 16384-block cache (36 GiB), an 8192-token
-    session of 512 records (1,207,959,552 bytes).  Save with GPU digests, restore into a fresh table: the
-    round trip is the identity, and every CRC32C and SHA-256 equals the oracle's over the pinned records."""
+    session of 512 records (1,207,959,552 bytes).  Save with GPU digests: all 512 pinned records equal the
+    oracle's gather over a host copy of the session's blocks (taken by torch's own indexing), and every CRC32C
+    and SHA-256 equals the oracle's.  Restore into a fresh table, then again with every block's CRC32C
+    checked in the copy (the checked restore at its default chunking: batched copies, two device slots,
+    placements on the aside stream): each time the target blocks equal the oracle's scatter, i.e. the
+    source blocks, and the checked restore's CRC32Cs pass."""
     caches, backing = synth.make_caches(36, 16384, layout="kv_split")
     size = 36 * 65536
     plane = planes(caches, capacity=512 * size + (64 << 20))
@@ -747,15 +735,32 @@ def test_qwen3_8b_8k_session_at_full_size(planes, oracle_lib):
     crcs, shas = oracle_lib.digest_records(staged.pointer, size, size, 512, threads=16)
     assert [crc for _, crc in got] == crcs.tolist()
     assert [sha for sha, _ in got] == [bytes(s).hex() for s in shas]
-    for index in (0, 301, 511):
-        record = pinned_bytes(staged, index * size, size)
-        for s, (offset, _, _, nbytes) in enumerate(plane.spans()):
-            assert np.array_equal(record[offset:offset + nbytes],
-                                  oracle_lib.fill_span(0, s, saved[index], nbytes, synth.KIND_BF16)), (index, s)
+    # The oracle's gather over host copies of the session's blocks, layer by layer ([2, 512, N, H, D] each,
+    # K half then V half, in the plane's sorted layer order): block j of the copy is block saved[j].
+    src, dst = torch.tensor(saved, device="cuda"), torch.tensor(restored, device="cuda")
+    copies, host_spans_ = [], []
+    for name, view in plane.caches.items():
+        host = view[:, src].contiguous().view(torch.uint8).cpu().numpy().reshape(-1)
+        half = host.size // 2
+        copies.append(host)
+        host_spans_ += [(host.ctypes.data, half // 512, None, half // 512),
+                        (host.ctypes.data + half, half // 512, None, half // 512)]
+    spans = [(base, pitch, offset, nbytes) for (base, pitch, _, nbytes), (offset, *_rest)
+             in zip(host_spans_, plane.spans())]
+    assert [s[3] for s in spans] == [s[3] for s in plane.spans()]
+    expected = oracle_lib.gather(spans, list(range(512)), size)
+    pinned = np.ctypeslib.as_array((C.c_uint8 * (512 * size)).from_address(staged.pointer)).reshape(512, size)
+    mismatched = [i for i in range(512) if not np.array_equal(pinned[i], expected[i])]
+    assert not mismatched, mismatched[:8]
+    del expected, copies
     assert plane.load_scatter(restored, targets) == 19
     torch.cuda.synchronize()
-    src, dst = torch.tensor(saved, device="cuda"), torch.tensor(restored, device="cuda")
     for view in caches.values():               # [2, blocks, N, H, D]
+        assert torch.equal(view[:, src].view(torch.int16), view[:, dst].view(torch.int16))
+        view[:, dst] = 0
+    assert plane.load_scatter_checked(restored, targets, [crc for _, crc in got]) == 19
+    torch.cuda.synchronize()
+    for view in caches.values():
         assert torch.equal(view[:, src].view(torch.int16), view[:, dst].view(torch.int16))
     staged.close()
 
@@ -887,10 +892,11 @@ def test_a_tensor_parallel_shard_round_trips_with_short_spans(planes, oracle_lib
     staged.close()
 
 
-def test_an_early_reported_restore_is_complete_for_the_engine_stream(planes):
+def early_report_scenario(planes):
     """The connector's protocol (reference vllm.py:454-466, 663-679): a loader thread runs the restore while the
     engine polls its progress; at most 128 MiB left, the load is reported and the next forward waits on the last
-    launch's event (wait_on_engine_stream).  Work on the engine stream after that wait sees every restored byte."""
+    launch's event (wait_on_engine_stream).  Checks that work on the engine stream after that wait sees every
+    restored byte; returns the slowest progress poll in seconds."""
     import threading
     import time
     from kvsnap_amd.ordering import EARLY_REPORT_BYTES, early_report
@@ -929,9 +935,6 @@ def test_an_early_reported_restore_is_complete_for_the_engine_stream(planes):
     assert report is not None and not failure
     left, last = report
     assert left <= EARLY_REPORT_BYTES
-    # Polling never waits for the copy (a query of the event the loader thread synchronized on
-    # used to be held until the whole 21 ms restore was over).
-    assert slowest < 0.005, slowest
     plane.wait_on_engine_stream(last)
     # The next "forward": reads of the restored blocks, queued on the engine stream.
     seen = [view[:, dst].clone() for view in caches.values()]
@@ -940,6 +943,13 @@ def test_an_early_reported_restore_is_complete_for_the_engine_stream(planes):
     for view, got in zip(caches.values(), seen):
         assert torch.equal(got.view(torch.int16), view[:, src].view(torch.int16))
     staged.close()
+    return slowest
+
+
+def test_an_early_reported_restore_is_complete_for_the_engine_stream(planes):
+    """The early-report protocol's ordering, with no wall-clock bound (the poll's latency is checked by
+    tests/test_zz_timing.py, collected after every parity test)."""
+    early_report_scenario(planes)
 
 
 @pytest.mark.parametrize("seed", range(6))
