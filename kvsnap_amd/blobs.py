@@ -19,15 +19,20 @@ GPU check (see ``TorchBlockDataPlane.load_scatter_verified``).
 from __future__ import annotations
 
 from concurrent.futures import ThreadPoolExecutor
+from contextlib import contextmanager
+import ctypes as C
+import errno
 import fcntl
 import os
 from pathlib import Path
+import re
 import struct
 import uuid
 
-from .native_io import get_io_backend
+from .native_io import NativeIO, get_io_backend
 
 HEADER = struct.Struct("<8sIQI8s")
+_BLOB_ID = re.compile("[0-9a-f]{64}")
 MAGIC = b"KVSBLOB1"
 VERSION = 1
 
@@ -57,12 +62,19 @@ class BlobDirectory:
         self.root = Path(root)
         self.blob_dir = self.root / "blobs"
         self.blob_dir.mkdir(parents=True, exist_ok=True)
+        self._blob_dir_str = str(self.blob_dir)
         self.io = get_io_backend(io_backend)
 
     def path(self, blob_id: str) -> Path:
-        if len(blob_id) != 64 or any(c not in "0123456789abcdef" for c in blob_id):
+        if type(blob_id) is not str or not _BLOB_ID.fullmatch(blob_id):
             raise CorruptSnapshotError("invalid blob identifier")
         return self.blob_dir / (blob_id + ".blob")
+
+    def _path_str(self, blob_id: str) -> str:
+        """:meth:`path` as a string (a read plan builds thousands of them; pathlib takes 4 us each)."""
+        if type(blob_id) is not str or not _BLOB_ID.fullmatch(blob_id):
+            raise CorruptSnapshotError("invalid blob identifier")
+        return f"{self._blob_dir_str}/{blob_id}.blob"
 
     def write_blob(self, blob_id, data, crc32c, *, durable=False):
         """Write one blob unless a file of that name already exists (content-addressed dedup).
@@ -206,9 +218,35 @@ class BlobDirectory:
             if type(offset) is not int or type(length) is not int or offset < 0 or length != block_bytes:
                 raise CorruptSnapshotError(f"segment {position} is not one KV block of the block size "
                                            f"({block_bytes} bytes)")
-            plan.append((self.path(segment["blob_id"]), address + position * block_bytes, HEADER.size + offset,
+            plan.append((self._path_str(segment["blob_id"]), address + position * block_bytes, HEADER.size + offset,
                          length, segment["crc32c"], block))
         return plan
+
+    @contextmanager
+    def ring_reader(self, segments, ring, block_bytes, per_chunk, slots, *, first_block=0, workers=8,
+                    verify="host"):
+        """Native threads reading ``segments`` (blocks ``first_block``, ...) into a ring of pinned chunk slots.
+
+        Chunk k is blocks ``[k * per_chunk, (k + 1) * per_chunk)`` of the
+        segments; it lands in slot ``k % slots`` of the ring at ``ring`` (each
+        slot ``per_chunk * block_bytes`` bytes).  The readers refill a slot only
+        after :meth:`BlobRingReader.release` of the chunk it held.  Under the
+        shared ``.blob.lock`` for the reader's lifetime; every header is checked
+        and, with ``verify="host"``, every block's CRC32C.  Needs the native
+        I/O backend.
+        """
+        if verify not in ("host", "none"):
+            raise ValueError("verify must be host or none")
+        if not isinstance(self.io, NativeIO):
+            raise RuntimeError("the ring reader needs the native I/O backend")
+        plan = self._read_plan(segments, 0, block_bytes, first_block)
+        with (self.root / ".blob.lock").open("a+b") as lock:
+            fcntl.flock(lock, fcntl.LOCK_SH)
+            reader = BlobRingReader(self.io, plan, block_bytes, ring, per_chunk, slots, workers, verify == "host")
+            try:
+                yield reader
+            finally:
+                reader.close()
 
     def read_prepared_into(self, segments, address, block_bytes, *, first_block=0, workers=8, verify="host"):
         """Read a snapshot's blocks from their blob files into packed pinned memory.
@@ -223,6 +261,15 @@ class BlobDirectory:
         """
         if verify not in ("host", "none"):
             raise ValueError("verify must be host or none")
+        if isinstance(self.io, NativeIO):
+            # One chunk of every block: ``workers`` native threads, none of them holding the interpreter lock.
+            if segments:
+                with self.ring_reader(segments, address, block_bytes, len(segments), 1, first_block=first_block,
+                                      workers=workers, verify=verify) as reader:
+                    reader.wait(0)
+            else:
+                self._read_plan(segments, address, block_bytes, first_block)
+            return
         plan = self._read_plan(segments, address, block_bytes, first_block)
         io = self.io
 
@@ -231,14 +278,14 @@ class BlobDirectory:
             try:
                 fd = os.open(path, os.O_RDONLY)
             except OSError as exc:
-                raise CorruptSnapshotError(f"unreadable blob {path.name}: {exc}") from exc
+                raise CorruptSnapshotError(f"unreadable blob {os.path.basename(path)}: {exc}") from exc
             try:
                 stored, _ = parse_header(io.pread_all(fd, HEADER.size, 0))
                 if payload_at - HEADER.size + length > stored:
-                    raise CorruptSnapshotError(f"block {block} runs past the payload of {path.name}")
+                    raise CorruptSnapshotError(f"block {block} runs past the payload of {os.path.basename(path)}")
                 io.pread_into(fd, target, length, payload_at)
             except OSError as exc:
-                raise CorruptSnapshotError(f"unreadable blob {path.name}: {exc}") from exc
+                raise CorruptSnapshotError(f"unreadable blob {os.path.basename(path)}: {exc}") from exc
             finally:
                 os.close(fd)
             if verify == "host" and io.crc32c_at(target, length) != crc:
@@ -249,3 +296,60 @@ class BlobDirectory:
             with ThreadPoolExecutor(max_workers=workers, thread_name_prefix="kvsnap-read") as pool:
                 for _ in pool.map(fetch, plan):
                     pass
+
+
+class BlobRingReader:
+    """The native blob ring reader (``kvsnap_blob_reader_*`` in ``libkvsnap_io.so``) over one read plan.
+
+    Errors are raised as :class:`CorruptSnapshotError` with the messages of
+    the Python read path: an unreadable blob, an invalid header, a block past
+    its blob's payload, a CRC32C mismatch.
+    """
+
+    def __init__(self, io, plan, block_bytes, ring, per_chunk, slots, workers, verify):
+        if type(per_chunk) is not int or type(slots) is not int or per_chunk < 1 or slots < 1:
+            raise ValueError("a ring needs at least one slot of at least one block")
+        if type(workers) is not int or not 1 <= workers <= 64:
+            raise ValueError("1-64 read workers")
+        self.lib, self.plan = io.lib, plan
+        n = len(plan)
+        self.chunks = -(-n // per_chunk)
+        names = [os.fsencode(job[0]) for job in plan]
+        self._paths = (C.c_char_p * n)(*names)
+        self._offsets = (C.c_uint64 * n)(*[job[2] - HEADER.size for job in plan])
+        self._crcs = (C.c_uint32 * n)(*[job[4] for job in plan])
+        self.handle = self.lib.kvsnap_blob_reader_start(
+            C.cast(self._paths, C.c_void_p), C.cast(self._offsets, C.c_void_p), C.cast(self._crcs, C.c_void_p), n,
+            block_bytes, ring, per_chunk, slots, workers, 1 if verify else 0)
+        if not self.handle:
+            raise RuntimeError("the blob ring reader could not be started")
+
+    def _raise(self, code, failed):
+        path, block = os.path.basename(self.plan[failed][0]), self.plan[failed][5]
+        if code == errno.EILSEQ:
+            raise CorruptSnapshotError(f"block {block} fails its checksum (CRC32C)")
+        if code == errno.ERANGE:
+            raise CorruptSnapshotError(f"block {block} runs past the payload of {path}")
+        if code == errno.EBADMSG:
+            raise CorruptSnapshotError(f"invalid blob header ({path})")
+        raise CorruptSnapshotError(f"unreadable blob {path}: {os.strerror(code)}")
+
+    def wait(self, k):
+        """Return once chunk k is in its slot; raise the first failure at or before chunk k's end."""
+        failed = C.c_int64(-1)
+        code = self.lib.kvsnap_blob_reader_wait(self.handle, k, C.byref(failed))
+        if code == errno.EINVAL and failed.value < 0:
+            raise ValueError(f"no chunk {k} in this read")
+        if code:
+            self._raise(code, failed.value)
+
+    def release(self, k):
+        """Chunk k's slot may be refilled (its bytes are copied out)."""
+        if self.lib.kvsnap_blob_reader_release(self.handle, k):
+            raise ValueError(f"no chunk {k} in this read")
+
+    def close(self):
+        """Stop the readers and wait for them: the ring may be freed afterwards."""
+        if self.handle:
+            handle, self.handle = self.handle, None
+            self.lib.kvsnap_blob_reader_finish(handle, None)

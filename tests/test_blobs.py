@@ -97,3 +97,85 @@ def test_blocks_written_from_memory_in_place_and_dedup_counts(tmp_path):
     child = blocks[:2] + records(1, 5000, seed=9)
     store.write_blocks(child, digests(child))
     assert store.written == 1 and len(list((tmp_path / "blobs").glob("*.blob"))) == 4
+
+
+def _chunk(blocks, k, per_chunk):
+    return b"".join(blocks[k * per_chunk:(k + 1) * per_chunk])
+
+
+@pytest.mark.parametrize("per_chunk,slots,workers", [(1, 2, 1), (4, 3, 7), (5, 2, 16), (64, 1, 8)])
+def test_the_ring_reader_fills_slots_in_order_and_never_before_their_release(tmp_path, per_chunk, slots, workers):
+    """Native readers fill chunk k into slot k % slots only after chunk k - slots was released: a slot still
+    holds its chunk's bytes however long the caller keeps it (here: past the time every other read takes)."""
+    import time
+    store = BlobDirectory(tmp_path, io_backend="native")
+    size = 6144
+    blocks = records(37, size, seed=11)
+    segments = store.write_blocks(blocks, digests(blocks))
+    ring = C.create_string_buffer(per_chunk * slots * size)
+    chunks = -(-37 // per_chunk)
+    with store.ring_reader(segments, C.addressof(ring), size, per_chunk, slots, workers=workers) as reader:
+        assert reader.chunks == chunks
+        for k in range(chunks):
+            reader.wait(k)
+            at = (k % slots) * per_chunk * size
+            want = _chunk(blocks, k, per_chunk)
+            assert ring.raw[at:at + len(want)] == want, k
+            time.sleep(0.01)                 # the readers may run ahead into the other slots, never into this one
+            assert ring.raw[at:at + len(want)] == want, k
+            reader.release(k)
+        with pytest.raises(ValueError):
+            reader.wait(chunks)
+
+
+def test_the_ring_reader_reports_each_failure_at_its_chunk_with_the_python_path_s_message(tmp_path):
+    """A bad block stops the read: the chunks before it still arrive whole; waiting on its chunk raises the
+    message the Python read path raises (checksum, header, payload range, unreadable file)."""
+    size = 4096
+    for damage, match in [("crc", "block 9 fails its checksum"), ("header", "invalid blob header"),
+                          ("short", "unreadable blob"), ("missing", "unreadable blob"),
+                          ("range", "block 9 runs past the payload")]:
+        folder = tmp_path / damage
+        store = BlobDirectory(folder, io_backend="native")
+        blocks = records(12, size, seed=12)
+        segments = store.write_blocks(blocks, digests(blocks))
+        path = folder / "blobs" / (segments[9]["blob_id"] + ".blob")
+        raw = bytearray(path.read_bytes())
+        if damage == "crc":
+            raw[40] ^= 1
+        elif damage == "header":
+            raw[0:8] = b"KVSBLOB9"
+        elif damage == "short":
+            raw = raw[:100]
+        elif damage == "range":
+            segments[9] = dict(segments[9], offset=8)
+        if damage == "missing":
+            os.unlink(path)
+        else:
+            path.write_bytes(bytes(raw))
+        ring = C.create_string_buffer(4 * 3 * size)
+        with store.ring_reader(segments, C.addressof(ring), size, 4, 3, workers=4) as reader:
+            for k in range(2):
+                reader.wait(k)
+                at = (k % 3) * 4 * size
+                assert ring.raw[at:at + 4 * size] == _chunk(blocks, k, 4), (damage, k)
+                reader.release(k)
+            with pytest.raises(CorruptSnapshotError, match=match):
+                reader.wait(2)
+
+
+def test_the_ring_reader_leaves_crc_checks_to_the_caller_when_asked(tmp_path):
+    store = BlobDirectory(tmp_path, io_backend="native")
+    blocks = records(3, 4096, seed=13)
+    segments = store.write_blocks(blocks, digests(blocks))
+    path = tmp_path / "blobs" / (segments[1]["blob_id"] + ".blob")
+    raw = bytearray(path.read_bytes())
+    raw[-1] ^= 1
+    path.write_bytes(bytes(raw))
+    ring = C.create_string_buffer(3 * 4096)
+    with store.ring_reader(segments, C.addressof(ring), 4096, 3, 1, verify="none") as reader:
+        reader.wait(0)
+    assert ring.raw[4096:8191] == blocks[1][:4095] and ring.raw[8191] == blocks[1][4095] ^ 1
+    with pytest.raises(RuntimeError, match="native"):
+        with BlobDirectory(tmp_path, io_backend="python").ring_reader(segments, C.addressof(ring), 4096, 3, 1):
+            pass
