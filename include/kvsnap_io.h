@@ -37,6 +37,33 @@ void kvsnap_io_pool_destroy(void* pool);
  * above the budget, ECANCELED while stopping.  io.cpp:135-154 */
 int kvsnap_io_pool_transfer(void* pool, int fd, void* data, size_t size, int64_t offset, int write, int durable);
 
+/* The blob ring reader: the disk stage of a restore (replaces the read
+ * threads of read_prepared_into, kvsnap/store/store.py:686-723, and their
+ * per-block kvsnap_io_pool_transfer calls, io.cpp:135-154).  `threads` native
+ * threads (1..64) take blocks 0..n_blocks-1 in order; block i is the payload
+ * range [payload_offsets[i], + block_bytes) of the blob file paths[i] (32-byte
+ * header "<8sIQI8s": "KVSBLOB1", version 1, payload length, CRC32C, 8 zero
+ * bytes), pread into the ring of `slots` slots of `per_chunk` blocks at
+ * ring + ((i / per_chunk) % slots) * per_chunk * block_bytes
+ * + (i % per_chunk) * block_bytes.  A block of chunk k >= slots waits for
+ * kvsnap_blob_reader_release(k - slots).  With `verify`, each block's
+ * CRC32C must equal crcs[i].  Paths and tables are copied; the ring is
+ * borrowed until kvsnap_blob_reader_finish returns.  NULL on bad arguments. */
+void* kvsnap_blob_reader_start(const char* const* paths, const uint64_t* payload_offsets, const uint32_t* crcs,
+                               int64_t n_blocks, uint64_t block_bytes, void* ring, int64_t per_chunk, int64_t slots,
+                               int threads, int verify);
+/* 0 once every block of chunk `chunk` is in its slot; else the error of the
+ * first failed block at or before the chunk's end (an errno from open/pread,
+ * EIO for a short file, EBADMSG for a bad header, ERANGE for a block past the
+ * payload, EILSEQ for a CRC32C mismatch), its index in *failed_block.  The
+ * first failure stops the reader.  EINVAL for a chunk out of range. */
+int kvsnap_blob_reader_wait(void* reader, int64_t chunk, int64_t* failed_block);
+/* Chunk `chunk`'s slot may be refilled. */
+int kvsnap_blob_reader_release(void* reader, int64_t chunk);
+/* Stops the threads, waits for them and frees the reader; returns the first
+ * failure (as kvsnap_blob_reader_wait) or 0. */
+int kvsnap_blob_reader_finish(void* reader, int64_t* failed_block);
+
 #ifdef __cplusplus
 }
 #endif

@@ -43,7 +43,7 @@ from dataclasses import dataclass, field
 import threading
 
 from .blobs import CorruptSnapshotError
-from .dataplane import CopyFailed
+from .dataplane import CopyFailed, StagingUnavailable
 from .layout import LayoutMismatch, require_layout
 from .native_io import get_io_backend
 from .ordering import EARLY_REPORT_BYTES, early_report
@@ -252,6 +252,8 @@ class KvsnapWorker:
                                             verify="host" if self.verify == "host" else "gpu")
             except CorruptSnapshotError:
                 raise      # found before that chunk's copy, after the earlier ones completed: a recompute miss
+            except StagingUnavailable as exc:
+                raise LoadRefused(f"no device staging for the load: {exc}") from exc     # before any copy
             except Exception as exc:
                 raise DMAUnknown("kvsnap H2D completion could not be proven") from exc
         with self.host_tier.borrow(segments, transfer.snapshot["locations"]) as sources:
@@ -267,6 +269,8 @@ class KvsnapWorker:
                 return plane.load_scatter(targets, sources, progress=progress)
             except CorruptSnapshotError:
                 raise      # a block failed the checked copy's CRC32C: none of them counts as loaded
+            except StagingUnavailable as exc:
+                raise LoadRefused(f"no device staging for the load: {exc}") from exc     # before any copy
             except Exception as exc:
                 raise DMAUnknown("kvsnap H2D completion could not be proven") from exc
 

@@ -33,6 +33,7 @@ torch = pytest.importorskip("torch")
 
 import oracle
 from kvsnap_amd import dataplane
+from kvsnap_amd.blobs import CorruptSnapshotError
 from kvsnap_amd.dataplane import TorchBlockDataPlane
 
 LAYERS, HEADS, TOKENS, WIDTH = 36, 8, 16, 256
@@ -79,6 +80,25 @@ class HostKernels:
         for i, block in enumerate(self._int64(blocks, n)):
             for offset, base, pitch, count in self._spans(offsets, bases, pitches, words, n_spans):
                 C.memmove(base + block * pitch, records + i * record_pitch + offset, 8 * count)
+        return 0
+
+    def kvsnap_restore_blocks_checked(self, sources, blocks, n, offsets, bases, pitches, words, n_spans, programs,
+                                      partial, stream):
+        """The checked restore: the copy, and (a stand-in for the per-span partials) each record's CRC32C in
+        its first partial slot, computed from the record bytes read."""
+        self.launches.append(("restore_checked", n))
+        spans = self._spans(offsets, bases, pitches, words, n_spans)
+        record_bytes = max(offset + 8 * count for offset, _, _, count in spans)
+        for i, (source, block) in enumerate(zip(self._int64(sources, n), self._int64(blocks, n))):
+            for offset, base, pitch, count in spans:
+                C.memmove(base + block * pitch, source + offset, 8 * count)
+            C.c_uint32.from_address(partial + 4 * i * n_spans).value = oracle.crc32c(C.string_at(source, record_bytes))
+        return 0
+
+    def kvsnap_restore_checked_crc32c(self, partial, n, offsets, words, n_spans, record_bytes, out, stream):
+        self.launches.append(("restore_checked_crc32c", n))
+        for i in range(n):
+            C.c_uint32.from_address(out + 4 * i).value = C.c_uint32.from_address(partial + 4 * i * n_spans).value
         return 0
 
     def kvsnap_zero_regions(self, base, starts, lengths, n, stream):
@@ -812,3 +832,153 @@ def test_restore_runs_group_consecutive_records():
     assert _runs([100, 110, 200], 10, 5) == [(5, 2), (7, 1)]
     assert _runs([30, 20, 10], 10) == [(0, 1), (1, 1), (2, 1)]
     assert _runs([], 10) == []
+
+
+# ---------------------------------------------------------------- device staging
+
+
+class NoDeviceMemory(CpuCuda):
+    """CpuCuda whose device allocations above 1 MiB fail as torch's do when the GPU is full."""
+
+    def empty(self, *args, **kwargs):
+        if kwargs.get("device") is CUDA:
+            count = args[0] if args and isinstance(args[0], int) else 1
+            if count > (1 << 20):
+                raise torch.OutOfMemoryError("CUDA out of memory. Tried to allocate 504.00 MiB")
+        return super().empty(*args, **kwargs)
+
+
+def test_a_copy_engine_restore_without_device_memory_is_refused_before_any_copy(host_kernels, monkeypatch):
+    """With no reserved staging and a full GPU, load_scatter (copy engines) and load_scatter_checked raise
+    StagingUnavailable before uploading or copying anything: no launch, no copy, the cache untouched."""
+    monkeypatch.setattr(dataplane, "PLACE_ASIDE", False)
+    caches = qwen3_8b_caches(12)
+    plane = plane_over(caches, restore_mode="dma")
+    plane.torch = NoDeviceMemory()
+    copies = []
+    host_kernels.kvsnap_copy_to_device = lambda *args: copies.append(args) or 0
+    sources = slabs(plane, 3, shared=True)
+    before = cache_bits(caches)
+    with pytest.raises(dataplane.StagingUnavailable, match="out of memory"):
+        plane.load_scatter([1, 2, 3], sources)
+    with pytest.raises(dataplane.StagingUnavailable):
+        plane.load_scatter_checked([1, 2, 3], sources, [0, 0, 0])
+    assert copies == [] and host_kernels.launches == []
+    after = cache_bits(caches)
+    assert all(torch.equal(after[name], before[name]) for name in caches)
+
+
+def test_restores_take_their_staging_from_the_reserve_and_allocate_nothing(host_kernels, monkeypatch):
+    """A plane holding its reserved device staging restores through the copy engines with every device
+    allocation failing: the slots are slices of the reserve, and the blocks land."""
+    monkeypatch.setattr(dataplane, "PLACE_ASIDE", False)        # copies and placements in turn, one stream
+    caches = qwen3_8b_caches(12)
+    plane = plane_over(caches, restore_mode="dma")
+    assert plane.device_staging_bytes == dataplane.DEVICE_STAGING_BYTES
+    plane._reserved_staging = torch.empty(4 * plane.block_bytes + (1 << 20), dtype=torch.uint8)
+    plane.torch = NoDeviceMemory()
+    size = plane.block_bytes
+    sources = slabs(plane, 3, shared=True)
+    for i, block in enumerate([4, 5, 6]):
+        for position, name in enumerate(sorted(caches)):
+            sources[i][0].fill(sources[i][1] + position * SPAN, span_of(caches[name], block))
+    assert plane.load_scatter([1, 2, 3], sources, chunk_bytes=size) == 3
+    for name in caches:
+        for target, block in zip([1, 2, 3], [4, 5, 6]):
+            assert span_of(caches[name], target) == span_of(caches[name], block)
+    assert plane._reserved_lock.acquire(blocking=False)       # handed back
+    plane._reserved_lock.release()
+
+
+def test_a_batched_checked_copy_engine_restore_keeps_its_slots_and_targets_apart(host_kernels, monkeypatch):
+    """load_scatter_checked at its default chunking through the copy engines, with more launches than
+    COPY_BATCH + COPY_TAIL (launches of two blocks here): copies grouped four launches at a time but the last
+    three, alternating between two device slots; each launch places and checks its blocks from its slot, at
+    its own offset, on the aside stream; a slot is copied into again only after the placements that read it.
+    Every target block holds its own source's bytes and every CRC32C passes; a wrong one fails that block."""
+    caches = qwen3_8b_caches(48, seed=9)
+    plane = plane_over(caches, restore_mode="dma")
+    plane.pool = Arena(160 << 20)
+    size = plane.block_bytes
+    monkeypatch.setattr(TorchBlockDataPlane, "_launch_bounds",
+                        lambda self, n, chunk_bytes: [(a, min(n, a + 2)) for a in range(0, n, 2)])
+    saved = list(range(1, 21))
+    restored = list(range(47, 27, -1))
+    sources = slabs(plane, 20, shared=True)
+    plane.save_gather(saved, sources, 20 * TOKENS)
+    crcs = [oracle.crc32c(sources[0][0].at(i * size, size)) for i in range(20)]
+    log = []
+
+    class Stream:
+        def __init__(self, name, handle):
+            self.name, self.cuda_stream = name, handle
+
+        def wait_event(self, event):
+            log.append((self.name, "waits", event.label))
+
+        def synchronize(self):
+            pass
+
+    class Event:
+        count = 0
+
+        def record(self, stream=None):
+            Event.count += 1
+            self.label = Event.count
+            log.append((stream.name, "records", self.label))
+
+        def synchronize(self):
+            pass
+
+        def query(self):
+            return True
+
+    copy, place = Stream("copy", 7), Stream("place", 9)
+    names = {7: "copy", 9: "place"}
+    plane._copy_stream = copy
+    plane.torch.cuda.Event = Event
+    to_device, checked = host_kernels.kvsnap_copy_to_device, host_kernels.kvsnap_restore_blocks_checked
+    slab_at = sources[0][0].pointer
+    slot_of = {}
+
+    def logged_copy(dst, src, nbytes, stream):
+        if slab_at <= src < slab_at + 20 * size:             # a record copy, not a table upload
+            first = (src - slab_at) // size
+            log.append((names[stream], "copies", first, nbytes // size))
+            for j in range(nbytes // size):
+                slot_of[first + j] = dst + j * size
+        return to_device(dst, src, nbytes, stream)
+
+    def logged_checked(sources_table, blocks, n, *rest):
+        reads = list((C.c_int64 * n).from_address(sources_table))
+        targets = list((C.c_int64 * n).from_address(blocks))
+        first = restored.index(targets[0])
+        # every block is read from where its own record was copied, and lands in its own target
+        assert reads == [slot_of[first + j] for j in range(n)], first
+        assert targets == restored[first:first + n]
+        log.append((names[rest[-1]], "checks", first, n))
+        return checked(sources_table, blocks, n, *rest)
+
+    with patch.object(host_kernels, "kvsnap_copy_to_device", logged_copy), \
+         patch.object(host_kernels, "kvsnap_restore_blocks_checked", logged_checked), \
+         patch.object(dataplane, "_drain", lambda torch, stream: None), \
+         patch.object(TorchBlockDataPlane, "_place_stream", lambda self: place):
+        assert plane.load_scatter_checked(restored, sources, crcs) == 10
+    copies = [entry[2:] for entry in log if entry[1] == "copies"]
+    assert copies == [(0, 8), (8, 6), (14, 2), (16, 2), (18, 2)]        # launches [0-3], [4-6], 7, 8, 9
+    checks = [entry[2:] for entry in log if entry[1] == "checks"]
+    assert checks == [(2 * k, 2) for k in range(10)] and all(e[0] == "place" for e in log if e[1] == "checks")
+    # the third copy (slot 0 again) waits for the event the place stream recorded after the first batch's checks
+    third = log.index(("copy", "copies", 14, 2))
+    waited = [e for e in log[:third] if e[0] == "copy" and e[1] == "waits"][-1][2]
+    last_check_of_first = max(i for i, e in enumerate(log) if e[:2] == ("place", "checks") and e[2] < 8)
+    assert ("place", "records", waited) in log[last_check_of_first:third]
+    for name in caches:
+        for target, block in zip(restored, saved):
+            assert span_of(caches[name], target) == span_of(caches[name], block), (name, target)
+    bad = list(crcs)
+    bad[5] ^= 1
+    with patch.object(dataplane, "_drain", lambda torch, stream: None), \
+         patch.object(TorchBlockDataPlane, "_place_stream", lambda self: place):
+        with pytest.raises(CorruptSnapshotError, match="first: block 5"):
+            plane.load_scatter_checked(restored, sources, bad)
