@@ -1020,6 +1020,8 @@ def run_kernels(args):
     work = torch.empty(work_bytes, dtype=torch.uint8, device="cuda")
     sha = torch.empty((session, 32), dtype=torch.uint8, device="cuda")
     hint = plane.min_span_bytes
+    records_at = torch.tensor([stage.data_ptr() + i * size for i in range(session)], dtype=torch.int64, device="cuda")
+    partial = torch.empty(session * tables[0].numel(), dtype=torch.int32, device="cuda")
     runs = {
         "plain_copy": (lambda: other.copy_(stage), 2 * total, args.reps),
         "gather_pieces_kernel": (lambda: gather_blocks(ids, *tables, stage.data_ptr(), size, min_span_bytes=hint),
@@ -1035,6 +1037,13 @@ def run_kernels(args):
                                                          min_span_bytes=hint), 2 * total, args.reps),
         "sha256_kernel": (lambda: _check(lib, lib.kvsnap_sha256_records(
             stage.data_ptr(), size, size, session, sha.data_ptr(), stream.cuda_stream)), total, 1),
+        # The gather with every record's CRC32C folded in, into device records on a full grid, and its finish
+        # (the save's record bytes and CRC32Cs from one read of the cache): read + write, like the gather.
+        "gather_checked_kernel": (lambda: (_check(lib, lib.kvsnap_gather_blocks_checked(
+            records_at.data_ptr(), ids.data_ptr(), session, *(t.data_ptr() for t in tables), tables[0].numel(), None,
+            0, 0, partial.data_ptr(), stream.cuda_stream)), _check(lib, lib.kvsnap_restore_checked_crc32c(
+                partial.data_ptr(), session, tables[0].data_ptr(), tables[3].data_ptr(), tables[0].numel(), size,
+                crc.data_ptr(), stream.cuda_stream))), 2 * total, args.reps),
     }
     out = {}
     for name, (fn, algorithmic, reps) in runs.items():
@@ -1043,6 +1052,12 @@ def run_kernels(args):
         out[name] = {"ms": round(ms, 4), "algorithmic_bytes": algorithmic,
                      "gbps": round(algorithmic / ms / 1e6, 1)}
     out["sha256_kernel"]["issue_roofline"] = sha_issue_bound(size, session, out["sha256_kernel"]["ms"])
+    # The checked gather's CRC32Cs against the CRC kernel's over the same records (the last run of each).
+    runs["crc_records_kernel"][0]()
+    want = crc.clone()
+    runs["gather_checked_kernel"][0]()
+    torch.cuda.synchronize()
+    out["gather_checked_kernel"]["crc32c_equal_crc_kernel"] = bool(torch.equal(want, crc))
     staged.close()
     plane.close()
     return {"workload": "kernels", "snapshot_bytes": total, "layout": args.layout, "kv_heads": args.kv_heads,

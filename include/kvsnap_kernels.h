@@ -55,6 +55,23 @@ int kvsnap_restore_blocks(const int64_t* sources, const int64_t* blocks, int64_t
                           const int64_t* span_words, int64_t n_spans, int64_t min_span_bytes, int programs,
                           uintptr_t stream);
 
+/* The save's gather with every record's CRC32C folded in (the checked
+ * restore's inverse): for every (block i, span s), copy span_words[s] words
+ * from span_bases[s] + blocks[i] * span_pitches[s] to dests[i] +
+ * span_offsets[s] (pinned host memory or device memory) and, when `stage` is
+ * not NULL, also to stage + i * stage_pitch + span_offsets[s] (device
+ * memory), and leave the span's raw CRC in partial[i * n_spans + s] for
+ * kvsnap_restore_checked_crc32c.  One wave per (block, span); `programs`
+ * caps the grid (<= 0: one workgroup per four jobs).  Replaces save_gather's
+ * index_select + cat and D2H (kvsnap/connector/dataplane.py:409-427) followed
+ * by the per-block host CRC32C (kvsnap/connector/volatile.py:151,
+ * kvsnap/store/store.py:622) for saves whose records are written straight
+ * into pinned memory. */
+int kvsnap_gather_blocks_checked(const int64_t* dests, const int64_t* blocks, int64_t n_blocks,
+                                 const int64_t* span_offsets, const int64_t* span_bases, const int64_t* span_pitches,
+                                 const int64_t* span_words, int64_t n_spans, void* stage, int64_t stage_pitch,
+                                 int programs, uint32_t* partial, uintptr_t stream);
+
 /* Checked restore: the copy of kvsnap_restore_blocks (any span length and
  * 8-byte alignment), and partial[i * n_spans + s] = the raw CRC32C (zero
  * initial value, no final xor) of block i's span s at the span's end, folded

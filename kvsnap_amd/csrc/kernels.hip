@@ -957,7 +957,11 @@ constexpr int kCheckedSlicing = 1024;             // S: slicing-by-4, [4][256]
 constexpr int kCheckedRowShift = 2048;            // M[64]: x^(128 k)
 constexpr int kCheckedLdsWords = kCheckedRowShift + 64;
 constexpr int kCheckedPowers = kCheckedLdsWords;  // x^(8 * 2^k), k < 48, read from global memory only
-constexpr int kCheckedTableWords = kCheckedPowers + 48;
+// x^(8 n) for n < 2^36 as three lookups: x^(8 j), x^(8 * 2^12 j) and x^(8 * 2^24 j), j < 4096.
+constexpr int kCheckedPow0 = kCheckedPowers + 48, kCheckedPow1 = kCheckedPow0 + 4096,
+              kCheckedPow2 = kCheckedPow1 + 4096;
+constexpr int kCheckedTableWords = kCheckedPow2 + 4096;
+constexpr uint64_t kCheckedMaxShift = uint64_t(1) << 36;
 
 __device__ uint32_t g_crc_checked_tables[kCheckedTableWords];
 
@@ -993,35 +997,33 @@ __device__ __forceinline__ void store_slot(char* p, u32x4 v) {
     __builtin_nontemporal_store(static_cast<uint64_t>(v.z) | (static_cast<uint64_t>(v.w) << 32), q + 1);
 }
 
-// Copy one span (nbytes a multiple of 8) with one wave and return this lane's
-// share of its raw CRC32C at the span's end.
-template <bool kWide>
+// Copy one span (nbytes a multiple of 8) with one wave, to `dst` and with
+// kTwo also to `dst2`, and return this lane's share of its raw CRC32C at the
+// span's end.  (Loading the next pass before folding this one measured no
+// faster, into HBM or over the link, and slowed the TP = 8 shard's gather.)
+template <bool kWide, bool kTwo>
 __device__ __forceinline__ uint32_t copy_span_crc(const char* __restrict__ src, char* __restrict__ dst,
-                                                  int64_t nbytes, int lane, const uint32_t* lds) {
+                                                  char* __restrict__ dst2, int64_t nbytes, int lane,
+                                                  const uint32_t* lds) {
     const uint32_t* slicing = lds + kCheckedSlicing;
     const int64_t slots = nbytes >> 4;
     uint32_t acc = 0;
     for (int64_t row = 0; row < slots; row += kCheckedUnroll * 64) {  // wave-uniform
         const int64_t i = row + lane;
+        const bool whole = row + kCheckedUnroll * 64 <= slots;
         u32x4 v[kCheckedUnroll];
-        if (row + kCheckedUnroll * 64 <= slots) {
 #pragma unroll
-            for (int u = 0; u < kCheckedUnroll; ++u) v[u] = load_slot<kWide>(src + 16 * (i + u * 64));
+        for (int u = 0; u < kCheckedUnroll; ++u)
+            v[u] = whole || i + u * 64 < slots ? load_slot<kWide>(src + 16 * (i + u * 64)) : u32x4{0u, 0u, 0u, 0u};
 #pragma unroll
-            for (int u = 0; u < kCheckedUnroll; ++u) store_slot<kWide>(dst + 16 * (i + u * 64), v[u]);
+        for (int u = 0; u < kCheckedUnroll; ++u)
+            if (whole || i + u * 64 < slots) {
+                store_slot<kWide>(dst + 16 * (i + u * 64), v[u]);
+                if (kTwo) store_slot<kWide>(dst2 + 16 * (i + u * 64), v[u]);
+            }
 #pragma unroll
-            for (int u = 0; u < kCheckedUnroll; ++u) acc = crc_advance(lds, acc) ^ crc_word_shared(slicing, v[u]);
-        } else {
-#pragma unroll
-            for (int u = 0; u < kCheckedUnroll; ++u)
-                v[u] = i + u * 64 < slots ? load_slot<kWide>(src + 16 * (i + u * 64)) : u32x4{0u, 0u, 0u, 0u};
-#pragma unroll
-            for (int u = 0; u < kCheckedUnroll; ++u)
-                if (i + u * 64 < slots) store_slot<kWide>(dst + 16 * (i + u * 64), v[u]);
-#pragma unroll
-            for (int u = 0; u < kCheckedUnroll; ++u)
-                if (i + u * 64 < slots) acc = crc_advance(lds, acc) ^ crc_word_shared(slicing, v[u]);
-        }
+        for (int u = 0; u < kCheckedUnroll; ++u)
+            if (whole || i + u * 64 < slots) acc = crc_advance(lds, acc) ^ crc_word_shared(slicing, v[u]);
     }
     const int r = static_cast<int>(slots & 63);
     uint32_t x = gf_mul(lds[kCheckedRowShift + ((r - 1 - lane) & 63)], acc);
@@ -1030,6 +1032,7 @@ __device__ __forceinline__ uint32_t copy_span_crc(const char* __restrict__ src, 
         if (lane == 0) {
             const uint64_t w = *reinterpret_cast<const uint64_t*>(src + 16 * slots);
             *reinterpret_cast<uint64_t*>(dst + 16 * slots) = w;
+            if (kTwo) *reinterpret_cast<uint64_t*>(dst2 + 16 * slots) = w;
             x ^= crc_dword_shared(slicing, crc_dword_shared(slicing, static_cast<uint32_t>(w)) ^
                                                static_cast<uint32_t>(w >> 32));
         }
@@ -1055,39 +1058,91 @@ __global__ __launch_bounds__(kRestoreThreads) void restore_checked_kernel(
         char* dst = reinterpret_cast<char*>(bases[s] + blocks[b] * pitches[s]);
         const int64_t nbytes = words[s] * 8;
         const bool wide = ((reinterpret_cast<uintptr_t>(src) | reinterpret_cast<uintptr_t>(dst)) & 15) == 0;
-        uint32_t x = wide ? copy_span_crc<true>(src, dst, nbytes, lane, lds)
-                          : copy_span_crc<false>(src, dst, nbytes, lane, lds);
+        uint32_t x = wide ? copy_span_crc<true, false>(src, dst, nullptr, nbytes, lane, lds)
+                          : copy_span_crc<false, false>(src, dst, nullptr, nbytes, lane, lds);
 #pragma unroll
         for (int o = 32; o > 0; o >>= 1) x ^= __shfl_xor(x, o);
         if (lane == 0) partial[job] = x;
     }
 }
 
-// x^(8 n) mod P from the powers x^(8 * 2^k), k < 48.
+// The save's gather with the CRC32C folded in, the checked restore's inverse:
+// one wave per (block, span) job copies the span from the cache to its record
+// at dests[b] (pinned host memory over the link, or device memory) and, with
+// kStage, also to stage + b * stage_pitch (device memory, for the SHA-256
+// kernels), and leaves the span's raw CRC in partial[job] for
+// restore_checked_finish_kernel.  One read of the cache gives the record, its
+// device copy and its CRC32C.
+//
+// Over the host link (a small grid of whole CUs) a workgroup is 1024 lanes:
+// one wave per SIMD waits out each pass's loads and folds, so sixteen keep a
+// CU's share of the link busy (a direct hashed save of 4 such workgroups ran
+// at 30 GB/s with 256-lane ones).  Into HBM (a full grid) it is 256 lanes.
+constexpr int kGatherLinkThreads = 1024;
+
+template <bool kStage, int kT>
+__global__ __launch_bounds__(kT) void gather_checked_kernel(
+    const int64_t* __restrict__ dests, const int64_t* __restrict__ blocks, int64_t n_blocks,
+    const int64_t* __restrict__ offs, const int64_t* __restrict__ bases, const int64_t* __restrict__ pitches,
+    const int64_t* __restrict__ words, int64_t n_spans, char* __restrict__ stage, int64_t stage_pitch,
+    uint32_t* __restrict__ partial) {
+    __shared__ uint32_t lds[kCheckedLdsWords];
+    for (int i = threadIdx.x; i < kCheckedLdsWords; i += kT) lds[i] = g_crc_checked_tables[i];
+    __syncthreads();
+    constexpr int kWaves = kT / 64;
+    const int lane = static_cast<int>(threadIdx.x) & 63;
+    const int64_t wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) >> 6);
+    const int64_t jobs = n_blocks * n_spans;
+    for (int64_t job = static_cast<int64_t>(blockIdx.x) * kWaves + wave; job < jobs;
+         job += static_cast<int64_t>(gridDim.x) * kWaves) {
+        const int64_t b = job / n_spans, s = job - b * n_spans;
+        const char* src = reinterpret_cast<const char*>(bases[s] + blocks[b] * pitches[s]);
+        char* dst = reinterpret_cast<char*>(dests[b] + offs[s]);
+        char* dst2 = kStage ? stage + b * stage_pitch + offs[s] : nullptr;
+        const int64_t nbytes = words[s] * 8;
+        const bool wide = ((reinterpret_cast<uintptr_t>(src) | reinterpret_cast<uintptr_t>(dst) |
+                            reinterpret_cast<uintptr_t>(dst2)) & 15) == 0;
+        uint32_t x = wide ? copy_span_crc<true, kStage>(src, dst, dst2, nbytes, lane, lds)
+                          : copy_span_crc<false, kStage>(src, dst, dst2, nbytes, lane, lds);
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) x ^= __shfl_xor(x, o);
+        if (lane == 0) partial[job] = x;
+    }
+}
+
+// x^(8 n) mod P for n < 2^36: two multiplications of three table entries.
 __device__ __forceinline__ uint32_t xpow8n(uint64_t n) {
-    uint32_t result = 0x80000000u;  // x^0
-    for (int k = 0; k < 48; ++k)
-        if ((n >> k) & 1) result = gf_mul(g_crc_checked_tables[kCheckedPowers + k], result);
-    return result;
+    const uint32_t* t = g_crc_checked_tables;
+    return gf_mul(gf_mul(t[kCheckedPow0 + (n & 4095u)], t[kCheckedPow1 + ((n >> 12) & 4095u)]),
+                  t[kCheckedPow2 + ((n >> 24) & 4095u)]);
 }
 
 // Record r's CRC32C from its spans' partials: span j's raw CRC moves from the
 // span's end to the record's, x^(8 (record_bytes - offset_j - bytes_j)), and
-// the initial ~0 adds init_term.  The shifts are the workgroup's first work,
-// in dynamic LDS, one span per lane.
-__global__ __launch_bounds__(64) void restore_checked_finish_kernel(
+// the initial ~0 adds init_term.  The shifts (the same for every record) are
+// the workgroup's first work, in dynamic LDS, one span per lane; then one
+// wave per record, its lanes over the record's spans, XOR-reduced.
+constexpr int kFinishThreads = 256;
+
+__global__ __launch_bounds__(kFinishThreads) void restore_checked_finish_kernel(
     const uint32_t* __restrict__ partial, int64_t n_records, const int64_t* __restrict__ offs,
     const int64_t* __restrict__ words, int64_t n_spans, uint64_t record_bytes, uint32_t init_term,
     uint32_t* __restrict__ out) {
     extern __shared__ uint32_t shifts[];
-    for (int64_t j = threadIdx.x; j < n_spans; j += 64)
+    for (int64_t j = threadIdx.x; j < n_spans; j += kFinishThreads)
         shifts[j] = xpow8n(record_bytes - static_cast<uint64_t>(offs[j]) - static_cast<uint64_t>(words[j]) * 8);
     __syncthreads();
-    const int64_t r = static_cast<int64_t>(blockIdx.x) * 64 + threadIdx.x;
-    if (r >= n_records) return;
-    uint32_t s = 0;
-    for (int64_t j = 0; j < n_spans; ++j) s ^= gf_mul(shifts[j], partial[r * n_spans + j]);
-    out[r] = ~(init_term ^ s);
+    constexpr int kWaves = kFinishThreads / 64;
+    const int lane = static_cast<int>(threadIdx.x) & 63;
+    const int64_t wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) >> 6);
+    for (int64_t r = static_cast<int64_t>(blockIdx.x) * kWaves + wave; r < n_records;
+         r += static_cast<int64_t>(gridDim.x) * kWaves) {
+        uint32_t x = 0;
+        for (int64_t j = lane; j < n_spans; j += 64) x ^= gf_mul(shifts[j], partial[r * n_spans + j]);
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) x ^= __shfl_xor(x, o);
+        if (lane == 0) out[r] = ~(init_term ^ x);
+    }
 }
 
 // ----------------------------------------------------------------- SHA-256 (FIPS 180-4)
@@ -1645,6 +1700,12 @@ void ensure_crc_tables() {
         }
     for (uint32_t k = 0; k < 64; ++k) checked[kCheckedRowShift + k] = host_xpow8n(16ull * k);
     for (uint32_t k = 0; k < 48; ++k) checked[kCheckedPowers + k] = host_xpow8n(1ull << k);
+    const uint32_t steps[3] = {host_xpow8n(1), host_xpow8n(1ull << 12), host_xpow8n(1ull << 24)};
+    for (int t = 0; t < 3; ++t) {
+        uint32_t* table = checked + kCheckedPow0 + 4096 * t;
+        table[0] = 0x80000000u;  // x^0
+        for (uint32_t j = 1; j < 4096; ++j) table[j] = host_gf_mul(table[j - 1], steps[t]);
+    }
     rc = hipMemcpyToSymbol(HIP_SYMBOL(g_crc_checked_tables), checked, sizeof checked, 0, hipMemcpyHostToDevice);
     if (rc != hipSuccess) throw std::runtime_error(std::string("CRC32C table upload: ") + hipGetErrorString(rc));
     g_tables_ready[device] = true;
@@ -1854,14 +1915,25 @@ uint32_t* static_crc_workspace() {
     return g_scratch_ptr[device];
 }
 
-// LDS a link-bound copy workgroup asks for and does not use.  With it no CU
-// can hold one of these workgroups beside a SHA-256 workgroup (133,120 of the
-// CU's 163,840 bytes), so the dispatcher keeps the copies off the hash
-// chains' CUs: a copy wave on a SIMD beside a round wave slows the chain
-// (SHA-256 range launches took 2.5-3.5 ms beside the restore kernel, 1.8 ms
-// alone).  The copies wait on the host link, not on their CUs.
-constexpr unsigned kCopyLdsFence = 32 * 1024;
-static_assert(kCopyLdsFence + sizeof(ShaSchedule) > 160 * 1024, "a copy and a SHA workgroup must not share a CU");
+// CUs to themselves.  A gfx950 CU has 160 KiB of LDS.  The kernels that hold
+// a few CUs for a long time -- the link-bound copies (a small grid whose waves
+// wait on the host link: the restore, the checked restore from pinned memory,
+// the gathers into pinned memory) and the SHA-256 chains (tens of ms) -- ask
+// for every byte of LDS they do not use, so no other workgroup that uses LDS
+// can share their CU.  Beside a copy wave a SHA-256 round wave slows (range
+// launches took 2.5-3.5 ms beside the restore kernel, 1.8 ms alone); and an
+// engine's workgroup placed beside a SHA-256 workgroup gets the VALU issue
+// slots its round waves leave (they issue in about 84 % of them), so a
+// decode step whose workgroups are dealt evenly over the chip waits for the
+// ones on those CUs (the synthetic decode's median step went from 0.80 to
+// 0.75 ms beside hashed saves once the SHA-256 workgroups took whole CUs).
+// The cost is a few CUs (one per SHA-256 group of 64 records, one per copy
+// workgroup) that the engine's LDS-using kernels leave alone.
+constexpr unsigned kCuLds = 160 * 1024;
+constexpr unsigned kCopyLdsFence = kCuLds;                                        // plain copies: no LDS of their own
+constexpr unsigned kCheckedLdsFence = kCuLds - sizeof(uint32_t) * kCheckedLdsWords;  // the checked copies' tables
+constexpr unsigned kShaLdsFence = kCuLds - sizeof(ShaSchedule);
+static_assert(sizeof(ShaSchedule) < kCuLds, "a SHA-256 workgroup fits a CU");
 
 }  // namespace
 
@@ -1907,6 +1979,48 @@ int kvsnap_restore_blocks(const int64_t* sources, const int64_t* blocks, int64_t
     });
 }
 
+int kvsnap_gather_blocks_checked(const int64_t* dests, const int64_t* blocks, int64_t n_blocks,
+                                 const int64_t* span_offsets, const int64_t* span_bases, const int64_t* span_pitches,
+                                 const int64_t* span_words, int64_t n_spans, void* stage, int64_t stage_pitch,
+                                 int programs, uint32_t* partial, uintptr_t stream) {
+    return guard([&] {
+        if (n_blocks < 0 || n_spans < 0) throw std::runtime_error("negative gather size");
+        if (n_blocks == 0 || n_spans == 0) return;
+        if (!dests || !blocks || !span_offsets || !span_bases || !span_pitches || !span_words || !partial)
+            throw std::runtime_error("checked gather tables and partials must be device pointers");
+        if (reinterpret_cast<uintptr_t>(partial) % 4) throw std::runtime_error("checked gather partials misaligned");
+        if (stage && (stage_pitch < 0 || reinterpret_cast<uintptr_t>(stage) % 8 || stage_pitch % 8))
+            throw std::runtime_error("checked gather stage must be 8-byte aligned with a non-negative pitch");
+        ensure_crc_tables();
+        // A small grid (programs > 0) writes over the host link: 1024-lane workgroups on whole CUs (the LDS
+        // fence).  A full grid is an HBM pass of 256-lane workgroups.
+        const bool link = programs > 0;
+        const int64_t waves = (link ? kGatherLinkThreads : kRestoreThreads) / 64;
+        const unsigned grid = grid_for((n_blocks * n_spans + waves - 1) / waves, programs);
+        const unsigned lds = link ? kCheckedLdsFence : 0;
+        hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+        char* stage_at = static_cast<char*>(stage);
+        const int64_t pitch = stage ? stage_pitch : 0;
+        if (link && stage)
+            hipLaunchKernelGGL((gather_checked_kernel<true, kGatherLinkThreads>), dim3(grid), dim3(kGatherLinkThreads),
+                               lds, s, dests, blocks, n_blocks, span_offsets, span_bases, span_pitches, span_words,
+                               n_spans, stage_at, pitch, partial);
+        else if (link)
+            hipLaunchKernelGGL((gather_checked_kernel<false, kGatherLinkThreads>), dim3(grid),
+                               dim3(kGatherLinkThreads), lds, s, dests, blocks, n_blocks, span_offsets, span_bases,
+                               span_pitches, span_words, n_spans, stage_at, pitch, partial);
+        else if (stage)
+            hipLaunchKernelGGL((gather_checked_kernel<true, kRestoreThreads>), dim3(grid), dim3(kRestoreThreads), lds,
+                               s, dests, blocks, n_blocks, span_offsets, span_bases, span_pitches, span_words, n_spans,
+                               stage_at, pitch, partial);
+        else
+            hipLaunchKernelGGL((gather_checked_kernel<false, kRestoreThreads>), dim3(grid), dim3(kRestoreThreads),
+                               lds, s, dests, blocks, n_blocks, span_offsets, span_bases, span_pitches, span_words,
+                               n_spans, stage_at, pitch, partial);
+        check_launch("checked gather");
+    });
+}
+
 int kvsnap_restore_blocks_checked(const int64_t* sources, const int64_t* blocks, int64_t n_blocks,
                                   const int64_t* span_offsets, const int64_t* span_bases, const int64_t* span_pitches,
                                   const int64_t* span_words, int64_t n_spans, int programs, uint32_t* partial,
@@ -1920,7 +2034,10 @@ int kvsnap_restore_blocks_checked(const int64_t* sources, const int64_t* blocks,
         ensure_crc_tables();
         constexpr int64_t waves = kRestoreThreads / 64;
         const unsigned grid = grid_for((n_blocks * n_spans + waves - 1) / waves, programs);
-        hipLaunchKernelGGL(restore_checked_kernel, dim3(grid), dim3(kRestoreThreads), kCopyLdsFence,
+        // From pinned memory (a small grid) the checked restore waits on the link and takes whole CUs; from
+        // device staging (programs <= 0, a full grid) it is an HBM pass and shares them.
+        hipLaunchKernelGGL(restore_checked_kernel, dim3(grid), dim3(kRestoreThreads),
+                           programs > 0 ? kCheckedLdsFence : 0,
                            reinterpret_cast<hipStream_t>(stream), sources, blocks, n_blocks, span_offsets,
                            span_bases, span_pitches, span_words, n_spans, partial);
         check_launch("checked restore");
@@ -1936,11 +2053,13 @@ int kvsnap_restore_checked_crc32c(const uint32_t* partial, int64_t n_blocks, con
         if (n_spans > kMaxCheckedSpans) throw std::runtime_error("too many spans for the checked restore");
         if (!out || (n_spans && (!partial || !span_offsets || !span_words)))
             throw std::runtime_error("checked restore CRC32C needs device pointers");
+        if (record_bytes >= kCheckedMaxShift) throw std::runtime_error("record too long for the checked CRC32C");
         ensure_crc_tables();
         const size_t lds = static_cast<size_t>(n_spans > 0 ? n_spans : 1) * sizeof(uint32_t);
-        hipLaunchKernelGGL(restore_checked_finish_kernel, dim3(static_cast<unsigned>((n_blocks + 63) / 64)),
-                           dim3(64), lds, reinterpret_cast<hipStream_t>(stream), partial, n_blocks, span_offsets,
-                           span_words, n_spans, record_bytes, host_shift(~0u, record_bytes), out);
+        const int64_t groups = (n_blocks + kFinishThreads / 64 - 1) / (kFinishThreads / 64);
+        hipLaunchKernelGGL(restore_checked_finish_kernel, dim3(static_cast<unsigned>(std::min<int64_t>(groups, 1024))),
+                           dim3(kFinishThreads), lds, reinterpret_cast<hipStream_t>(stream), partial, n_blocks,
+                           span_offsets, span_words, n_spans, record_bytes, host_shift(~0u, record_bytes), out);
         check_launch("checked restore CRC32C");
     });
 }
@@ -2166,9 +2285,9 @@ int kvsnap_sha256_ranges(int count, const uint64_t* records, const uint64_t* rec
         hipStream_t s = reinterpret_cast<hipStream_t>(stream);
         const dim3 grid(static_cast<unsigned>(groups), static_cast<unsigned>(used));
         if (aligned)
-            hipLaunchKernelGGL(sha256_ranges_kernel<true>, grid, dim3(kShaThreads), 0, s, ranges);
+            hipLaunchKernelGGL(sha256_ranges_kernel<true>, grid, dim3(kShaThreads), kShaLdsFence, s, ranges);
         else
-            hipLaunchKernelGGL(sha256_ranges_kernel<false>, grid, dim3(kShaThreads), 0, s, ranges);
+            hipLaunchKernelGGL(sha256_ranges_kernel<false>, grid, dim3(kShaThreads), kShaLdsFence, s, ranges);
         check_launch("sha256 ranges");
     });
 }
@@ -2186,10 +2305,10 @@ int kvsnap_sha256_records_range(const void* records, uint64_t record_bytes, uint
         const auto* base = static_cast<const uint8_t*>(records);
         auto* words = reinterpret_cast<uint32_t*>(out);
         if (aligned)
-            hipLaunchKernelGGL(sha256_kernel<true>, dim3(grid), dim3(kShaThreads), 0, s, base, record_bytes,
+            hipLaunchKernelGGL(sha256_kernel<true>, dim3(grid), dim3(kShaThreads), kShaLdsFence, s, base, record_bytes,
                                record_pitch, n_records, first_block, end_block, state, words);
         else
-            hipLaunchKernelGGL(sha256_kernel<false>, dim3(grid), dim3(kShaThreads), 0, s, base, record_bytes,
+            hipLaunchKernelGGL(sha256_kernel<false>, dim3(grid), dim3(kShaThreads), kShaLdsFence, s, base, record_bytes,
                                record_pitch, n_records, first_block, end_block, state, words);
         check_launch("sha256");
     });

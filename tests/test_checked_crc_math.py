@@ -120,3 +120,29 @@ def test_a_whole_rows_lane_shift_fails_on_a_short_last_row():
     spans, size = tiling([1024])                         # whole rows: both shifts agree
     record = bytes(rng.randrange(256) for _ in range(size))
     assert record_crc(record, spans, lane_shift=lambda r, lane: 63 - lane) == oracle.crc32c(record)
+
+
+def test_the_finish_kernel_s_three_table_shift_equals_shifting_zero_bytes():
+    """restore_checked_finish_kernel's x^(8 n) for n < 2^36 is the product of three table entries, x^(8 j),
+    x^(8 * 2^12 j) and x^(8 * 2^24 j) with j < 4096, each table built by repeated multiplication from x^0.
+    Checked against appending n zero bytes to a register (the definition) for small n, and against squaring for
+    large n; a table built one step short (x^(8 (j - 1))) must fail."""
+    steps = [xpow8n(1), xpow8n(1 << 12), xpow8n(1 << 24)]
+    tables = []
+    for step in steps:
+        table = [0x80000000]
+        for _ in range(4095):
+            table.append(gf_mul(table[-1], step))
+        tables.append(table)
+
+    def three(n, t=tables):
+        return gf_mul(gf_mul(t[0][n & 4095], t[1][(n >> 12) & 4095]), t[2][(n >> 24) & 4095])
+
+    rng = random.Random(41)
+    for n in [0, 1, 2, 7, 4095, 4096, 4097, 9000] + [rng.randrange(1 << 14) for _ in range(6)]:
+        state = rng.getrandbits(32)
+        assert gf_mul(three(n), state) == raw_crc(bytes(n), state), n
+    for n in [2359296, 2359296 - 65536, (1 << 36) - 1, rng.randrange(1 << 36)]:
+        assert three(n) == xpow8n(n), n
+    short = [[t[0]] + t[:-1] for t in tables]
+    assert three(9000, short) != three(9000)

@@ -95,6 +95,31 @@ class HostKernels:
             C.c_uint32.from_address(partial + 4 * i * n_spans).value = oracle.crc32c(C.string_at(source, record_bytes))
         return 0
 
+    def kvsnap_gather_blocks_checked(self, dests, blocks, n, offsets, bases, pitches, words, n_spans, stage,
+                                     stage_pitch, programs, partial, stream):
+        """The checked gather: each record to its destination (and to ``stage``), and (as the checked restore's
+        stand-in does) its CRC32C in its first partial slot."""
+        self.launches.append(("gather_checked", n))
+        spans = self._spans(offsets, bases, pitches, words, n_spans)
+        record_bytes = max(offset + 8 * count for offset, _, _, count in spans)
+        for i, (dest, block) in enumerate(zip(self._int64(dests, n), self._int64(blocks, n))):
+            for offset, base, pitch, count in spans:
+                C.memmove(dest + offset, base + block * pitch, 8 * count)
+                if stage:
+                    C.memmove(stage + i * stage_pitch + offset, base + block * pitch, 8 * count)
+            C.c_uint32.from_address(partial + 4 * i * n_spans).value = oracle.crc32c(C.string_at(dest, record_bytes))
+        return 0
+
+    def kvsnap_crc32c_workspace_bytes(self, record_bytes, n):
+        return 16
+
+    def kvsnap_crc32c_records(self, records, record_bytes, pitch, n, prior, out, workspace, work_bytes, stream):
+        self.launches.append(("crc32c", n))
+        for i in range(n):
+            C.c_uint32.from_address(out + 4 * i).value = oracle.crc32c(C.string_at(records + i * pitch, record_bytes),
+                                                                       prior)
+        return 0
+
     def kvsnap_restore_checked_crc32c(self, partial, n, offsets, words, n_spans, record_bytes, out, stream):
         self.launches.append(("restore_checked_crc32c", n))
         for i in range(n):
@@ -533,7 +558,7 @@ def test_digests_are_returned_in_block_order():
         """The oracle in place of the GPU hash job, behind the same interface."""
 
         def __init__(self, torch_module, records_ptr, record_bytes, record_pitch, n, device, lane, slice_blocks, *,
-                     timer=None, keepalive=None):
+                     timer=None, keepalive=None, crc=None):
             crcs, shas = oracle.digest_records(records_ptr, record_bytes, record_pitch, n)
             self.crc, self.sha = torch.from_numpy(crcs.astype(np.int64)), torch.from_numpy(shas)
 
@@ -982,3 +1007,50 @@ def test_a_batched_checked_copy_engine_restore_keeps_its_slots_and_targets_apart
          patch.object(TorchBlockDataPlane, "_place_stream", lambda self: place):
         with pytest.raises(CorruptSnapshotError, match="first: block 5"):
             plane.load_scatter_checked(restored, sources, bad)
+
+
+@pytest.mark.parametrize("tokens", [3 * TOKENS, 3 * TOKENS - 5])
+def test_a_hashed_direct_save_gathers_records_stage_and_crcs_in_one_pass(host_kernels, tokens):
+    """A direct save with digests: the checked gather writes every pinned record and its device copy (the SHA-256
+    kernels' input) from one read of the cache and gives the CRC32Cs; the hash job gets those CRC32Cs and
+    launches only the SHA-256.  With a partial last block, its tail is zeroed in both copies and its CRC32C is
+    taken again: every CRC32C equals the oracle's over the pinned record, and the device copy equals it."""
+    caches = qwen3_8b_caches(6, seed=4)
+    plane = plane_over(caches, save_mode="direct")
+    size = plane.block_bytes
+    seen = {}
+
+    class Job:
+        def __init__(self, torch_module, records_ptr, record_bytes, record_pitch, n, device, lane, slice_blocks, *,
+                     timer=None, keepalive=None, crc=None):
+            seen.update(records=C.string_at(records_ptr, n * record_bytes), crc=crc)
+            self.crc = crc
+            self.sha = torch.zeros((n, 32), dtype=torch.uint8)
+
+        def query(self):
+            return True
+
+        def finished(self, timeout=None):
+            return True
+
+        def synchronize(self):
+            pass
+
+    targets = slabs(plane, 3, shared=True)
+    digests = []
+    with patch.object(dataplane, "HashJob", Job), \
+         patch.object(TorchBlockDataPlane, "_hash_lane", lambda self: MagicMock()):
+        assert plane.save_gather([5, 2, 4], targets, tokens, digests=digests) == 1
+    assert [kind for kind, _ in host_kernels.launches if kind.startswith("gather")] == ["gather_checked"]
+    pinned = targets[0][0].at(0, 3 * size)
+    assert seen["records"] == pinned
+    for i, block in enumerate([5, 2, 4]):
+        assert pinned[i * size:i * size + SPAN] == (span_of(caches[sorted(caches)[0]], block) if i < 2 or
+                                                     tokens % TOKENS == 0 else pinned[i * size:i * size + SPAN])
+    crcs = [int(c) & 0xFFFFFFFF for c in seen["crc"].view(torch.int32).tolist()]
+    assert crcs == [oracle.crc32c(pinned[i * size:(i + 1) * size]) for i in range(3)]
+    if tokens % TOKENS:
+        want = bytearray(span_of(caches[sorted(caches)[0]], 4))
+        want[(tokens % TOKENS) * HEADS * WIDTH * 2:] = bytes(len(want) - (tokens % TOKENS) * HEADS * WIDTH * 2)
+        assert pinned[2 * size:2 * size + SPAN] == bytes(want)
+        assert ("crc32c", 1) in host_kernels.launches

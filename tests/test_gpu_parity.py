@@ -815,6 +815,93 @@ def test_the_checked_restore_kernel_gives_every_record_s_crc32c_and_the_restore_
     staging.close()
 
 
+@pytest.mark.parametrize("layers,layout,dtype,block_size,heads,head_dim,shift,to_host,with_stage,programs", [
+    (4, "vllm", "bf16", 16, 8, 128, 0, True, True, 4),        # 64 KiB spans into pinned memory, and a device copy
+    (4, "kv_split", "bf16", 16, 8, 128, 8, True, False, 4),   # 32 KiB spans, destinations 8 bytes off 16
+    (4, "kv_split", "fp8", 16, 8, 128, 0, False, True, 0),    # 16 KiB spans, device to device, full grid
+    (4, "kv_split", "bf16", 16, 1, 40, 0, False, False, 0),   # 1280-byte spans: a short last row
+    (4, "vllm", "bf16", 3, 1, 4, 0, True, True, 2),           # 48-byte spans
+    (4, "kv_split", "bf16", 3, 1, 4, 8, False, True, 0),      # 24-byte spans: an 8-byte word; 8-byte alignment
+    (36, "kv_split", "bf16", 16, 1, 128, 0, False, True, 0),  # a TP = 8 shard of Qwen3-8B: 72 spans of 4 KiB
+])
+def test_the_checked_gather_kernel_gives_the_oracle_s_records_and_crc32cs(
+        planes, oracle_lib, layers, layout, dtype, block_size, heads, head_dim, shift, to_host, with_stage, programs):
+    """kvsnap_gather_blocks_checked + kvsnap_restore_checked_crc32c through the C-ABI: every record written (into
+    pinned memory over the link, or device memory; and its device copy when asked) equals the oracle's gather of
+    the same blocks, and every record's CRC32C equals the oracle's (csrc/dataplane/io.cpp:39-44), over spans of
+    every length class the kernel handles; the cache is only read."""
+    torch_dtype = torch.bfloat16 if dtype == "bf16" else torch.float8_e4m3fn
+    caches, backing = synth.make_caches(layers, 64, block_size=block_size, heads=heads, head_dim=head_dim,
+                                        dtype=torch_dtype, layout=layout)
+    raw = backing.view(torch.uint8)
+    generator = torch.Generator(device="cuda").manual_seed(15)
+    raw.copy_(torch.randint(0, 256, raw.shape, dtype=torch.uint8, device="cuda", generator=generator))
+    plane = planes(caches, block_size=block_size)
+    size, n = plane.block_bytes, 29
+    blocks = random.Random(17).sample(range(64), n)
+    before = host_copy(backing)
+    expected = oracle_lib.gather(host_spans(plane, backing, before), blocks, size)
+    if to_host:
+        staging = plane.pool.reserve(n * size + 16)
+        base, host = staging.pointer + shift, None
+    else:
+        host = torch.zeros(n * size + 16, dtype=torch.uint8, device="cuda")
+        base, staging = host.data_ptr() + shift, None
+    stage = torch.zeros(n * size, dtype=torch.uint8, device="cuda") if with_stage else None
+    tables = plane._load_tables()
+    n_spans = tables[0].numel()
+    lib = kernel_library()
+    table = torch.tensor([base + i * size for i in range(n)] + blocks, dtype=torch.int64, device="cuda")
+    partial = torch.full((n * n_spans,), -1, dtype=torch.int32, device="cuda")
+    out = torch.zeros(n, dtype=torch.int32, device="cuda")
+    stream = torch.cuda.current_stream().cuda_stream
+    for first, last in ((0, 17), (17, n)):      # two launches, each writing its blocks' partials
+        _check(lib, lib.kvsnap_gather_blocks_checked(
+            table.data_ptr() + 8 * first, table.data_ptr() + 8 * (n + first), last - first,
+            *(t.data_ptr() for t in tables), n_spans, stage.data_ptr() + first * size if with_stage else None, size,
+            programs, partial.data_ptr() + 4 * first * n_spans, stream))
+    _check(lib, lib.kvsnap_restore_checked_crc32c(partial.data_ptr(), n, tables[0].data_ptr(), tables[3].data_ptr(),
+                                                  n_spans, size, out.data_ptr(), stream))
+    torch.cuda.synchronize()
+    if to_host:
+        written = np.ctypeslib.as_array((C.c_uint8 * (n * size)).from_address(base)).reshape(n, size).copy()
+        staging.close()
+    else:
+        written = host.cpu().numpy()[shift:shift + n * size].reshape(n, size)
+    assert np.array_equal(written, expected)
+    if with_stage:
+        assert np.array_equal(stage.cpu().numpy().reshape(n, size), expected)
+    assert [value & 0xFFFFFFFF for value in out.tolist()] == [oracle_lib.crc32c(r.tobytes()) for r in expected]
+    assert np.array_equal(host_copy(backing), before)
+
+
+@pytest.mark.parametrize("tokens", [12 * BLOCK_SIZE, 12 * BLOCK_SIZE - 7])
+def test_a_hashed_direct_save_is_one_checked_gather_and_its_digests_are_the_oracle_s(planes, oracle_lib, tokens):
+    """save_mode="direct" with digests: the checked gather writes the pinned records and their device copy and
+    folds their CRC32Cs in one pass over the cache; the SHA-256 reads the device copy.  Records (last tail zeroed),
+    CRC32Cs and SHA-256s equal the oracle's."""
+    caches, backing = synth.make_caches(LAYERS, 40, layout="kv_split")
+    plane = planes(caches, save_mode="direct", restore_programs=4)
+    keep = synth.fill(plane, 29)
+    torch.cuda.synchronize()
+    del keep
+    saved, _ = synth.block_tables(40, 12)
+    size = plane.block_bytes
+    before = host_copy(backing)
+    expected = oracle_lib.gather(host_spans(plane, backing, before), saved, size)
+    staged = plane.pool.reserve(12 * size)
+    digests = []
+    assert plane.save_gather(saved, [(staged, i * size) for i in range(12)], tokens, digests=digests) == 1
+    got = digests[0].result()
+    if tokens % BLOCK_SIZE:
+        oracle_lib.zero_tail(expected[11], plane.layers, tokens % BLOCK_SIZE)
+    pinned = np.ctypeslib.as_array((C.c_uint8 * (12 * size)).from_address(staged.pointer)).reshape(12, size).copy()
+    assert np.array_equal(pinned, expected)
+    crcs, shas = oracle_lib.digest_records(staged.pointer, size, size, 12, threads=8)
+    assert got == [(bytes(h).hex(), int(c)) for h, c in zip(shas, crcs)]
+    staged.close()
+
+
 @pytest.mark.parametrize("restore_mode", ["kernel", "dma"])
 def test_a_checked_restore_loads_clean_blocks_and_reports_a_corrupt_one_only_after_the_copy(planes, oracle_lib,
                                                                                            restore_mode):
