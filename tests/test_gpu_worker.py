@@ -190,3 +190,68 @@ def test_a_worker_that_registers_vllm_s_caches_saves_and_loads_what_the_oracle_s
         torch.cuda.synchronize()
         if worker.dataplane is not None:
             worker.dataplane.close()
+
+
+def test_the_vllm_connector_class_saves_and_loads_what_the_oracle_says(hip_library, oracle_lib, tmp_path):
+    """KvsnapConnector (KVConnectorBase_V1, worker role), imported through stand-in vLLM modules as vLLM would
+    build it from its KV-transfer config: register_kv_caches, then one durable save (blob files under
+    store_path) and its load into other blocks through the connector's hooks; the snapshot's ids and CRC32Cs
+    equal the oracle's digests, and the cache equals the oracle's scatter of the oracle's records."""
+    import importlib
+    import sys
+    from unittest.mock import patch
+    from test_connector import BASE, stand_in_vllm, vllm_config
+    with patch.dict(sys.modules, stand_in_vllm()):
+        sys.modules.pop("kvsnap_amd.connector", None)
+        connector_module = importlib.import_module("kvsnap_amd.connector")
+    sys.modules.pop("kvsnap_amd.connector", None)
+    role = stand_in_vllm()[BASE].KVConnectorRole
+    caches, backing = synth.make_caches(LAYERS, BLOCKS, layout="kv_split")
+    connector = connector_module.KvsnapConnector(vllm_config(tmp_path, pinned_pool_bytes=160 << 20,
+                                                             host_tier_bytes=64 << 20), role.WORKER, None)
+    try:
+        connector.register_kv_caches(caches)
+        plane = connector.worker.dataplane
+        keep = synth.fill(plane, 8)
+        torch.cuda.synchronize()
+        del keep
+        rng = random.Random(14)
+        source = rng.sample(range(1, BLOCKS), 20)
+        target = rng.sample([b for b in range(1, BLOCKS) if b not in source], 20)
+        tokens = 20 * BLOCK_SIZE - 3
+        size = plane.block_bytes
+        host = backing.view(torch.uint8).cpu().numpy().reshape(-1).copy()
+        base = backing.data_ptr()
+        host_spans = [(host.ctypes.data + (s[1] - base), s[2], s[0], s[3]) for s in plane.spans()]
+        records = oracle_lib.gather(host_spans, source, size)
+        oracle_lib.zero_tail(records[-1], plane.layers, tokens % BLOCK_SIZE)
+
+        Metadata = connector_module.KvsnapConnectorMetadata
+        connector.bind_connector_metadata(Metadata(saves=[Transfer("s", source, durability="durable",
+                                                                   num_kv_tokens=tokens)]))
+        connector.wait_for_save()
+        connector.clear_connector_metadata()
+        run_until(connector, lambda sending, receiving: "s" in sending, finished={"s"})
+        run_until(connector, lambda sending, receiving: not connector.worker._saves)
+        snapshot = connector.build_connector_worker_meta().prepared["s"]
+        crcs, shas = oracle_lib.digest_records(records.ctypes.data, size, size, len(source), threads=4)
+        assert [(s["blob_id"], s["crc32c"]) for s in snapshot["segments"]] == \
+            [(bytes(h).hex(), int(c)) for h, c in zip(shas, crcs)]
+        assert all((tmp_path / "blobs" / (s["blob_id"] + ".blob")).is_file() for s in snapshot["segments"])
+
+        connector.bind_connector_metadata(Metadata(loads=[Transfer("l", target, snapshot=snapshot,
+                                                                   durability="durable")]))
+        connector.start_load_kv(None)
+        connector.clear_connector_metadata()
+        run_until(connector, lambda sending, receiving: "l" in receiving)
+        run_until(connector, lambda sending, receiving: not connector.worker._loads)
+        torch.cuda.synchronize()
+        report = connector.build_connector_worker_meta()
+        assert report.loaded == ["l"] and report.failed_loads == []
+        oracle_lib.scatter(host_spans, target, [records.ctypes.data + i * size for i in range(len(target))])
+        after = backing.view(torch.uint8).cpu().numpy().reshape(-1)
+        changed = np.flatnonzero(after != host)
+        assert changed.size == 0, f"{changed.size} bytes differ from the oracle's scatter, first at {changed[0]}"
+    finally:
+        torch.cuda.synchronize()
+        connector.shutdown()
