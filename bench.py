@@ -76,6 +76,20 @@ SHA_VALU_PER_BLOCK = 596
 SHA_CYCLES_PER_VALU = 4
 SHA_ROUND_CYCLES = 37.5
 ENGINE_CLOCK_GHZ = 2.4
+# A floor that does not come from the kernel: FIPS 180-4's round in gfx950
+# instructions.  A round is six 32-bit additions (T1 = h + Sigma1 + Ch + (W+K),
+# e = d + T1, T2 = Sigma0 + Maj, a = T1 + T2; W+K comes summed from the message
+# schedule), two Sigma functions of three rotations XORed, and Ch and Maj.  With
+# v_add3_u32 (two additions), v_alignbit_b32 (a rotation) and v_bitop3_b32 (any
+# three-input boolean function) that is 3 + 2 * (3 + 1) + 2 = 13 instructions.
+# One lane per record issues all 13 in turn; split over two lanes of one wave
+# (which run one instruction stream), at best half of them each, rounded up,
+# plus one instruction that hands a value to the partner lane: 8.  The chain of
+# a record is then 64 rounds of 8 wave64 instructions a block, plus the 8
+# additions of the feed-forward (4 a lane).
+SHA_FIPS_ROUND_INSTRUCTIONS = 13
+SHA_FIPS_TWO_LANE_ROUND = (SHA_FIPS_ROUND_INSTRUCTIONS + 1) // 2 + 1
+SHA_FIPS_FEED_FORWARD = 4
 
 
 def sha_issue_bound(record_bytes, records, ms):
@@ -84,7 +98,16 @@ def sha_issue_bound(record_bytes, records, ms):
     bound_ms = blocks * SHA_VALU_PER_BLOCK * SHA_CYCLES_PER_VALU / (ENGINE_CLOCK_GHZ * 1e6)
     total = record_bytes * records
     sequence_ms = blocks * 64 * SHA_ROUND_CYCLES / (ENGINE_CLOCK_GHZ * 1e6)
+    fips_ms = blocks * (64 * SHA_FIPS_TWO_LANE_ROUND + SHA_FIPS_FEED_FORWARD) * SHA_CYCLES_PER_VALU / (
+        ENGINE_CLOCK_GHZ * 1e6)
+    one_lane_ms = blocks * (64 * SHA_FIPS_ROUND_INSTRUCTIONS + 2 * SHA_FIPS_FEED_FORWARD) * SHA_CYCLES_PER_VALU / (
+        ENGINE_CLOCK_GHZ * 1e6)
     return {"bound": "valu-issue (one chain per record)", "valu_per_block": SHA_VALU_PER_BLOCK,
+            "fips_floor": {"instructions_per_round": SHA_FIPS_ROUND_INSTRUCTIONS,
+                           "two_lane_instructions_per_round": SHA_FIPS_TWO_LANE_ROUND,
+                           "two_lane_floor_ms": round(fips_ms, 3), "frac": round(fips_ms / ms, 4),
+                           "one_lane_floor_ms": round(one_lane_ms, 3),
+                           "source": "FIPS 180-4 round operations in gfx950 instructions (add3, alignbit, bitop3)"},
             "cycles_per_valu": SHA_CYCLES_PER_VALU, "clock_ghz": ENGINE_CLOCK_GHZ, "bound_ms": round(bound_ms, 3),
             "achieved": round(total / (ms * 1e6), 2), "peak": round(total / (bound_ms * 1e6), 2), "unit": "GB/s",
             "frac": round(bound_ms / ms, 4), "round_cycles_measured": SHA_ROUND_CYCLES,
@@ -482,6 +505,11 @@ def run_save_restore(args):
         "save_ms": round(lat["save"], 3),
         "save_gbps": round(total / lat["save"] / 1e6, 2),
         "save_hashed_ms": round(lat["hashed"], 3),
+        # The same digests on this box's host cores instead (SHA-NI and SSE4.2 over the pinned records once the
+        # D2H has landed, the reference's way): the save, then the CPU baseline's SHA-256 and CRC32C legs.
+        "hashes_ready_host_ms": None if cpu is None else {
+            threads: round(lat["save"] + cpu["legs_ms"]["sha256"][threads] + cpu["legs_ms"]["crc32c"][threads], 3)
+            for threads in cpu["legs_ms"]["sha256"]},
         "save_plain_ms": round(lat["save_plain"], 3),
         "restore_ms": round(lat["restore"], 3),
         "restore_gbps": round(total / lat["restore"] / 1e6, 2),
@@ -530,16 +558,15 @@ def run_save_restore(args):
     }
     staged.close()
     plane.close()
+    del plane, staged, targets, tables
+    torch.cuda.empty_cache()
     if not args.no_disk_fork:
-        # The fourth workload at full size on the same caches (their seed-0 contents untouched by the restores,
-        # which only wrote the target blocks with the source blocks' bytes).
-        del plane, staged, targets
-        torch.cuda.empty_cache()
+        # The fourth workload at full size on the same caches.
         out["disk_fork"] = disk_fork(args, caches)
+    del caches, backing
+    torch.cuda.empty_cache()
     if not args.no_rotating:
-        # The fifth workload beside this one, in the same line: the 8k cache freed first.
-        del plane, caches, backing, staged, targets, tables
-        torch.cuda.empty_cache()
+        # The fifth workload beside this one, in the same line.
         rotating = run_rotating(args, hashed=True)
         out["rotating_fp8"] = {key: rotating[key] for key in (
             "metric", "value", "unit", "copy_alone_gbps", "rounds", "record_bytes", "sessions_tokens",
@@ -554,11 +581,18 @@ def run_save_restore(args):
         duplex = getattr(args, "duplex_result", None)
         process = "its own, run before this one touched the GPU"
         if duplex is None:
-            duplex, process = run_duplex(args), "this one (its third plane)"
+            duplex, process = run_duplex(args), "this one (a later plane)"
         out["duplex"] = {key: duplex[key] for key in (
             "metric", "value", "unit", "steps", "ms_per_step", "duplex_link_gbps", "restore_mode", "save_mode",
             "restore_stream_check", "parity", "streams")}
         out["duplex"]["process"] = process
+        if duplex is args.duplex_result:
+            # The same workload again in this process, whose earlier planes (the 8k plane, the disk-fork plane
+            # and the rotating fp8 plane) created their streams first: what a process's later plane finds.
+            later = run_duplex(args)
+            out["duplex"]["in_this_process"] = {key: later[key] for key in (
+                "value", "ms_per_step", "duplex_link_gbps", "restore_stream_check", "parity")}
+            out["duplex"]["in_this_process"]["plane"] = "the fourth plane of the bench process"
     out["hw_queues"] = os.environ.get("GPU_MAX_HW_QUEUES")
     return out
 
@@ -570,16 +604,11 @@ def run_disk_fork(args):
     from kvsnap_amd import synth
     from kvsnap_amd.dataplane import TorchBlockDataPlane
     caches, backing = synth.make_caches(36, 16384, block_size=16, layout=args.layout)
-    plane = TorchBlockDataPlane(caches, 16, 16 << 20)
-    keep = synth.fill(plane, 0)
-    torch.cuda.synchronize()
-    del keep
-    plane.close()
     return disk_fork(args, caches)
 
 
 def disk_fork(args, caches):
-    """The fourth workload on 16384-block Qwen3-8B caches (filled with seed 0): a 32k-token parent session
+    """The fourth workload on 16384-block Qwen3-8B caches (filled here with seed 0): a 32k-token parent session
     (2048 records, 4,831,838,208 B) and a forked child whose first 1536 blocks hold the parent's bytes in blocks
     of its own, each saved as blob files (GPU gather, D2H, GPU CRC32C + SHA-256 ids, content-addressed writes:
     2560 blobs), then the child restored from disk into fresh blocks by the pipelined reader with every block's
@@ -600,6 +629,12 @@ def disk_fork(args, caches):
     ring, chunk = 4, 128 << 20
     plane = TorchBlockDataPlane(caches, block_size, n * size + ring * chunk + (64 << 20), restore_mode="dma")
     plane.warm_up()
+    # Seed-0 contents in every block (an earlier workload's restores copied blocks onto others, and a parent
+    # holding two equal blocks would dedup within itself).
+    from kvsnap_amd import synth
+    keep = synth.fill(plane, 0)
+    torch.cuda.synchronize()
+    del keep
     parent = random.Random(1).sample(range(1, num_blocks), n)
     taken = set(parent)
     fresh = random.Random(3).sample([b for b in range(1, num_blocks) if b not in taken], n - shared)

@@ -1010,20 +1010,31 @@ __device__ __forceinline__ uint32_t copy_span_crc(const char* __restrict__ src, 
     uint32_t acc = 0;
     for (int64_t row = 0; row < slots; row += kCheckedUnroll * 64) {  // wave-uniform
         const int64_t i = row + lane;
-        const bool whole = row + kCheckedUnroll * 64 <= slots;
         u32x4 v[kCheckedUnroll];
+        if (row + kCheckedUnroll * 64 <= slots) {
 #pragma unroll
-        for (int u = 0; u < kCheckedUnroll; ++u)
-            v[u] = whole || i + u * 64 < slots ? load_slot<kWide>(src + 16 * (i + u * 64)) : u32x4{0u, 0u, 0u, 0u};
+            for (int u = 0; u < kCheckedUnroll; ++u) v[u] = load_slot<kWide>(src + 16 * (i + u * 64));
 #pragma unroll
-        for (int u = 0; u < kCheckedUnroll; ++u)
-            if (whole || i + u * 64 < slots) {
+            for (int u = 0; u < kCheckedUnroll; ++u) {
                 store_slot<kWide>(dst + 16 * (i + u * 64), v[u]);
                 if (kTwo) store_slot<kWide>(dst2 + 16 * (i + u * 64), v[u]);
             }
 #pragma unroll
-        for (int u = 0; u < kCheckedUnroll; ++u)
-            if (whole || i + u * 64 < slots) acc = crc_advance(lds, acc) ^ crc_word_shared(slicing, v[u]);
+            for (int u = 0; u < kCheckedUnroll; ++u) acc = crc_advance(lds, acc) ^ crc_word_shared(slicing, v[u]);
+        } else {
+#pragma unroll
+            for (int u = 0; u < kCheckedUnroll; ++u)
+                v[u] = i + u * 64 < slots ? load_slot<kWide>(src + 16 * (i + u * 64)) : u32x4{0u, 0u, 0u, 0u};
+#pragma unroll
+            for (int u = 0; u < kCheckedUnroll; ++u)
+                if (i + u * 64 < slots) {
+                    store_slot<kWide>(dst + 16 * (i + u * 64), v[u]);
+                    if (kTwo) store_slot<kWide>(dst2 + 16 * (i + u * 64), v[u]);
+                }
+#pragma unroll
+            for (int u = 0; u < kCheckedUnroll; ++u)
+                if (i + u * 64 < slots) acc = crc_advance(lds, acc) ^ crc_word_shared(slicing, v[u]);
+        }
     }
     const int r = static_cast<int>(slots & 63);
     uint32_t x = gf_mul(lds[kCheckedRowShift + ((r - 1 - lane) & 63)], acc);
