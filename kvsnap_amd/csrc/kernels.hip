@@ -997,17 +997,34 @@ __device__ __forceinline__ void store_slot(char* p, u32x4 v) {
     __builtin_nontemporal_store(static_cast<uint64_t>(v.z) | (static_cast<uint64_t>(v.w) << 32), q + 1);
 }
 
+// s_waitcnt vmcnt(0): every vector memory access of the wave so far has
+// completed (on gfx9 the counter covers stores too).
+constexpr unsigned kWaitMemory = 0x0F70;
+
 // Copy one span (nbytes a multiple of 8) with one wave, to `dst` and with
 // kTwo also to `dst2`, and return this lane's share of its raw CRC32C at the
 // span's end.  (Loading the next pass before folding this one measured no
 // faster, into HBM or over the link, and slowed the TP = 8 shard's gather.)
-template <bool kWide, bool kTwo>
+//
+// kPaced, for writes into pinned host memory: each slot's stores wait until
+// the wave's earlier accesses have completed, so a wave has one slot's
+// writes in flight.  Sixteen waves a CU issuing a whole pass of host writes
+// at once queue more than the link drains, and the queue holds up other
+// CUs' HBM traffic: a decode step beside such a save ran twice its time
+// (p99 stall 1.45 ms, rotating fp8 workload); paced, 0.14 ms, and the save
+// still fills its share of the link (41-44 GB/s on 4 workgroups).
+template <bool kWide, bool kTwo, bool kPaced>
 __device__ __forceinline__ uint32_t copy_span_crc(const char* __restrict__ src, char* __restrict__ dst,
                                                   char* __restrict__ dst2, int64_t nbytes, int lane,
                                                   const uint32_t* lds) {
     const uint32_t* slicing = lds + kCheckedSlicing;
     const int64_t slots = nbytes >> 4;
     uint32_t acc = 0;
+    auto store = [&](int64_t at, const u32x4& v) {
+        if (kPaced) __builtin_amdgcn_s_waitcnt(kWaitMemory);
+        store_slot<kWide>(dst + at, v);
+        if (kTwo) store_slot<kWide>(dst2 + at, v);
+    };
     for (int64_t row = 0; row < slots; row += kCheckedUnroll * 64) {  // wave-uniform
         const int64_t i = row + lane;
         u32x4 v[kCheckedUnroll];
@@ -1015,10 +1032,7 @@ __device__ __forceinline__ uint32_t copy_span_crc(const char* __restrict__ src, 
 #pragma unroll
             for (int u = 0; u < kCheckedUnroll; ++u) v[u] = load_slot<kWide>(src + 16 * (i + u * 64));
 #pragma unroll
-            for (int u = 0; u < kCheckedUnroll; ++u) {
-                store_slot<kWide>(dst + 16 * (i + u * 64), v[u]);
-                if (kTwo) store_slot<kWide>(dst2 + 16 * (i + u * 64), v[u]);
-            }
+            for (int u = 0; u < kCheckedUnroll; ++u) store(16 * (i + u * 64), v[u]);
 #pragma unroll
             for (int u = 0; u < kCheckedUnroll; ++u) acc = crc_advance(lds, acc) ^ crc_word_shared(slicing, v[u]);
         } else {
@@ -1027,10 +1041,7 @@ __device__ __forceinline__ uint32_t copy_span_crc(const char* __restrict__ src, 
                 v[u] = i + u * 64 < slots ? load_slot<kWide>(src + 16 * (i + u * 64)) : u32x4{0u, 0u, 0u, 0u};
 #pragma unroll
             for (int u = 0; u < kCheckedUnroll; ++u)
-                if (i + u * 64 < slots) {
-                    store_slot<kWide>(dst + 16 * (i + u * 64), v[u]);
-                    if (kTwo) store_slot<kWide>(dst2 + 16 * (i + u * 64), v[u]);
-                }
+                if (i + u * 64 < slots) store(16 * (i + u * 64), v[u]);
 #pragma unroll
             for (int u = 0; u < kCheckedUnroll; ++u)
                 if (i + u * 64 < slots) acc = crc_advance(lds, acc) ^ crc_word_shared(slicing, v[u]);
@@ -1069,8 +1080,8 @@ __global__ __launch_bounds__(kRestoreThreads) void restore_checked_kernel(
         char* dst = reinterpret_cast<char*>(bases[s] + blocks[b] * pitches[s]);
         const int64_t nbytes = words[s] * 8;
         const bool wide = ((reinterpret_cast<uintptr_t>(src) | reinterpret_cast<uintptr_t>(dst)) & 15) == 0;
-        uint32_t x = wide ? copy_span_crc<true, false>(src, dst, nullptr, nbytes, lane, lds)
-                          : copy_span_crc<false, false>(src, dst, nullptr, nbytes, lane, lds);
+        uint32_t x = wide ? copy_span_crc<true, false, false>(src, dst, nullptr, nbytes, lane, lds)
+                          : copy_span_crc<false, false, false>(src, dst, nullptr, nbytes, lane, lds);
 #pragma unroll
         for (int o = 32; o > 0; o >>= 1) x ^= __shfl_xor(x, o);
         if (lane == 0) partial[job] = x;
@@ -1113,8 +1124,10 @@ __global__ __launch_bounds__(kT) void gather_checked_kernel(
         const int64_t nbytes = words[s] * 8;
         const bool wide = ((reinterpret_cast<uintptr_t>(src) | reinterpret_cast<uintptr_t>(dst) |
                             reinterpret_cast<uintptr_t>(dst2)) & 15) == 0;
-        uint32_t x = wide ? copy_span_crc<true, kStage>(src, dst, dst2, nbytes, lane, lds)
-                          : copy_span_crc<false, kStage>(src, dst, dst2, nbytes, lane, lds);
+        // Into pinned memory (the link-bound shape) the writes are paced; into HBM they are not.
+        constexpr bool kPaced = kT == kGatherLinkThreads;
+        uint32_t x = wide ? copy_span_crc<true, kStage, kPaced>(src, dst, dst2, nbytes, lane, lds)
+                          : copy_span_crc<false, kStage, kPaced>(src, dst, dst2, nbytes, lane, lds);
 #pragma unroll
         for (int o = 32; o > 0; o >>= 1) x ^= __shfl_xor(x, o);
         if (lane == 0) partial[job] = x;
