@@ -600,10 +600,8 @@ def run_save_restore(args):
 # ---------------------------------------------------------------- disk-staged restore with fork dedup
 
 def run_disk_fork(args):
-    import torch
     from kvsnap_amd import synth
-    from kvsnap_amd.dataplane import TorchBlockDataPlane
-    caches, backing = synth.make_caches(36, 16384, block_size=16, layout=args.layout)
+    caches, _ = synth.make_caches(36, 16384, block_size=16, layout=args.layout)
     return disk_fork(args, caches)
 
 
