@@ -706,16 +706,52 @@ __device__ __forceinline__ int crc_lead(int64_t start) {
 // Issue the loads of the first batch of the stripe of `groups` groups at record offset `start` into `a`.
 // Chain c takes groups lead + c, lead + c + kCrcChains, ...  Only the first batch may hold front padding,
 // and only the last may hold fewer groups than chains.
+//
+// Aligned records take one path without branches.  A chain past the stripe's groups loads the stripe's
+// last group again, a word of front padding loads the record's first word, and crc_stripe_rest zeroes them
+// once the loads have landed (crc_first_words_kept).  The host sends records of fewer than 16 bytes, or of
+// 2 GiB or more, down the unaligned path, so every offset here is a record word's and fits 32 bits: the
+// loads take the record's address from scalar registers and one 32-bit offset a chain from a vector
+// register.  (With two load paths into the same registers the compiler waited for every earlier load, the
+// table words' included, before issuing these, and HBM sat idle for the table words' round trip; zeroing
+// here would wait for these loads before the tables are filled.)
+// Only the first chain can hold padding (less than a group of it lies before the first group loaded).
+__device__ __forceinline__ void crc_first_words_kept(int64_t start, int groups, uint32_t lane, u32x4* a) {
+    const int g = crc_lead(start);
+    const int count = groups - g < kCrcChains ? groups - g : kCrcChains;
+#pragma unroll
+    for (int c = 1; c < kCrcChains; ++c)
+        if (c >= count) a[c] = u32x4{0u, 0u, 0u, 0u};  // wave-uniform
+    const int64_t at = start + static_cast<int64_t>(g) * kCrcGroup;  // in (-1024, 2^31)
+    if (static_cast<int>(lane) * kCrcRun < -static_cast<int>(at)) a[0] = u32x4{0u, 0u, 0u, 0u};
+}
+
 template <bool kAligned>
 __device__ __forceinline__ void crc_stripe_first(const uint8_t* __restrict__ rec, int64_t start, int groups,
                                                  uint32_t lane, u32x4* a) {
+    static_assert(kCrcRunWords == 1, "one word per chain and batch");
     const int g = crc_lead(start);
     const int count = groups - g < kCrcChains ? groups - g : kCrcChains;
     const int64_t at = start + static_cast<int64_t>(g) * kCrcGroup;
-    if (kAligned && at >= 0 && count == kCrcChains)
-        crc_load_batch(rec, at, lane, a);
-    else
-        crc_load_any<kAligned>(rec, at, count, lane, a);
+    if (!kAligned) {
+        crc_load_any<false>(rec, at, count, lane, a);
+        return;
+    }
+    const int at32 = static_cast<int>(at);  // in (-1024, 2^31)
+    // An opaque copy of the record's address (in the global address space, so the loads stay global loads):
+    // loads through the kernel's read-only argument count as invariant, and the compiler moved them past
+    // the table fill and its barrier, to where they are used.
+    using GlobalByte = const __attribute__((address_space(1))) uint8_t;
+    using GlobalWord = const __attribute__((address_space(1))) u32x4;
+    GlobalByte* base = (GlobalByte*)rec;
+    asm volatile("" : "+s"(base));
+#pragma unroll
+    for (int c = 0; c < kCrcChains; ++c) {
+        const int cc = c < count ? c : count - 1;
+        int off = at32 + cc * kCrcGroup + static_cast<int>(lane) * kCrcRun;
+        off = off < 0 ? 0 : off;
+        a[c] = __builtin_nontemporal_load((GlobalWord*)(base + static_cast<uint32_t>(off)));
+    }
 }
 
 // One wave's job: the raw CRC of the stripe of `groups` groups whose first byte is at record offset
@@ -736,6 +772,7 @@ __device__ __forceinline__ uint32_t crc_stripe_rest(const uint32_t* lds, uint32_
     // The first batch's loads are complete before the steady state starts, which the wait for its
     // prefetches then counts on (vmcnt(0); expcnt and lgkmcnt left alone).
     __builtin_amdgcn_s_waitcnt(0x0F70);
+    if (kAligned) crc_first_words_kept(start, groups, lane, a);
     while (true) {
         if (g + 2 * kCrcChains > groups) {
             crc_fold_rest<kAligned>(lds, cols, rec, start, groups, g, count, lane, a, acc);
@@ -814,8 +851,11 @@ __global__ __launch_bounds__(kCrcThreads) void crc_stripes_kernel(const uint8_t*
         // tables are filled.
         const CrcTableWords words = crc_table_words();
         lane_shift = g_crc_tables[kCrcLaneShift + lane];
+        // Issued by every wave, a wave without a job loading job 0's: under a branch the compiler would
+        // count these loads as maybe not issued and have the fill wait for them.
         u32x4 a[kCrcBatchWords];
-        if (first < jobs) crc_stripe_first<kAligned>(job_record(first), job_start(first), groups, lane, a);
+        const uint32_t any = first < jobs ? first : 0;
+        crc_stripe_first<kAligned>(job_record(any), job_start(any), groups, lane, a);
         crc_fill_tables(lds, words);
         cols = crc_columns(lane);
         crc_tables_ready();
@@ -896,12 +936,14 @@ __global__ __launch_bounds__(kCrcThreads) void crc_records_kernel(const uint8_t*
         // tables are filled.
         const CrcTableWords words = crc_table_words();
         lane_shift = g_crc_tables[kCrcLaneShift + lane];
+        // Issued by every wave, a wave without a record this round loading record 0's stripe: under a branch
+        // the compiler would count these loads as maybe not issued and have the fill wait for them.
         u32x4 a[kCrcBatchWords];
         const int rec_in_round = wave / stripes, j = wave - rec_in_round * stripes;
-        if (rec_in_round < per_group && first + rec_in_round < n_records)
-            crc_stripe_first<kAligned>(records + (first + rec_in_round) * pitch,
-                                       static_cast<int64_t>(j) * groups * kCrcGroup - static_cast<int64_t>(pad),
-                                       groups, lane, a);
+        const int64_t r = rec_in_round < per_group && first + rec_in_round < n_records ? first + rec_in_round : 0;
+        crc_stripe_first<kAligned>(records + r * pitch,
+                                   static_cast<int64_t>(j) * groups * kCrcGroup - static_cast<int64_t>(pad), groups,
+                                   lane, a);
         crc_fill_tables(lds, words);
         cols = crc_columns(lane);
         crc_tables_ready();
@@ -1872,8 +1914,10 @@ bool crc_in_group(const CrcPlan& plan, int64_t n_records) {
 // words per record) is used unless the stripes combine in their workgroup.
 void launch_crc32c(const void* records, uint64_t record_bytes, uint64_t record_pitch, int64_t n_records,
                    uint32_t prior, uint32_t* out, uint32_t* partial, const CrcPlan& plan, hipStream_t s) {
+    // The aligned kernels load 16-byte words at 32-bit record offsets, and a record of fewer than 16 bytes
+    // has no word to stand in for a stripe's padding (crc_stripe_first).
     const bool aligned = (reinterpret_cast<uintptr_t>(records) % 16 == 0) && (record_pitch % 16 == 0) &&
-                         (record_bytes % 16 == 0);
+                         (record_bytes % 16 == 0) && record_bytes >= 16 && record_bytes < (uint64_t(1) << 31);
     const int64_t jobs = n_records * plan.stripes;
     if (jobs > (int64_t(1) << 31)) throw std::runtime_error("CRC32C: too many records in one call");
     const auto* base = static_cast<const uint8_t*>(records);
