@@ -1025,7 +1025,7 @@ def run_kernels(args):
     import torch
     from kvsnap_amd import synth
     from kvsnap_amd.dataplane import (_check, copy_host_blocks, digest_device_records, gather_blocks,
-                                      kernel_library, scatter_blocks, TorchBlockDataPlane)
+                                      gather_crc32c_launcher, kernel_library, scatter_blocks, TorchBlockDataPlane)
 
     layers, num_blocks, block_size, tokens = 36, 16384, 16, 8192
     session = tokens // block_size
@@ -1082,6 +1082,14 @@ def run_kernels(args):
             partial.data_ptr(), session, tables[0].data_ptr(), tables[3].data_ptr(), tables[0].numel(), size,
             crc.data_ptr(), stream.cuda_stream)), 4 * session * tables[0].numel(), args.reps),
     }
+    # The gather with CRC32C into device records (whole-KiB spans): the CRC32C kernel's stripes and tables with
+    # its loads from the cache and its words written to the records, one launch; read + write, like the gather.
+    groups = plane.group_tables()
+    if groups is not None:
+        fused = torch.empty(total, dtype=torch.uint8, device="cuda")
+        fused_crc = torch.empty(session, dtype=torch.int32, device="cuda")
+        runs["gather_crc_kernel"] = (gather_crc32c_launcher(ids, *groups, size, fused.data_ptr(), size, fused_crc),
+                                     2 * total, args.reps)
     out = {}
     for name, (fn, algorithmic, reps) in runs.items():
         fn()
@@ -1095,6 +1103,12 @@ def run_kernels(args):
     runs["gather_checked_kernel"][0]()
     torch.cuda.synchronize()
     out["gather_checked_kernel"]["crc32c_equal_crc_kernel"] = bool(torch.equal(want, crc))
+    if groups is not None:     # its records against the gather kernel's, its CRC32Cs against the CRC kernel's
+        runs["gather_pieces_kernel"][0]()
+        runs["gather_crc_kernel"][0]()
+        torch.cuda.synchronize()
+        out["gather_crc_kernel"]["records_equal_gather"] = bool(torch.equal(fused, stage))
+        out["gather_crc_kernel"]["crc32c_equal_crc_kernel"] = bool(torch.equal(want, fused_crc))
     staged.close()
     plane.close()
     return {"workload": "kernels", "snapshot_bytes": total, "layout": args.layout, "kv_heads": args.kv_heads,

@@ -72,6 +72,25 @@ int kvsnap_gather_blocks_checked(const int64_t* dests, const int64_t* blocks, in
                                  const int64_t* span_words, int64_t n_spans, void* stage, int64_t stage_pitch,
                                  int programs, uint32_t* partial, uintptr_t stream);
 
+/* Whether kvsnap_gather_crc32c takes records of record_bytes: 1 for whole
+ * KiB under 2 GiB, else 0. */
+int kvsnap_gather_crc32c_fits(uint64_t record_bytes);
+
+/* The save's gather into device records with every record's CRC32C, in one
+ * HBM pass: record i (block blocks[i]) to out + i * out_pitch, its CRC32C
+ * (init/xorout ~0) to crcs[i].  For layouts whose spans are whole KiB: the
+ * record's 1 KiB group g comes from group_bases[g] + blocks[i] *
+ * group_pitches[g] (16-byte aligned; record_bytes / 1024 groups, built once
+ * per layout from the span table).  out and out_pitch 16-byte aligned.
+ * Replaces save_gather's index_select + cat into device staging
+ * (kvsnap/connector/dataplane.py:409-417) together with the per-block
+ * CRC32C of each record (kvsnap/connector/volatile.py:151,
+ * kvsnap/store/store.py:622), which otherwise reads the staged records
+ * again. */
+int kvsnap_gather_crc32c(const int64_t* blocks, int64_t n_blocks, const int64_t* group_bases,
+                         const int64_t* group_pitches, uint64_t record_bytes, void* out, int64_t out_pitch,
+                         uint32_t* crcs, uintptr_t stream);
+
 /* Checked restore: the copy of kvsnap_restore_blocks (any span length and
  * 8-byte alignment), and partial[i * n_spans + s] = the raw CRC32C (zero
  * initial value, no final xor) of block i's span s at the span's end, folded

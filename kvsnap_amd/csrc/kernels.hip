@@ -757,11 +757,36 @@ __device__ __forceinline__ void crc_stripe_first(const uint8_t* __restrict__ rec
 // One wave's job: the raw CRC of the stripe of `groups` groups whose first byte is at record offset
 // `start` (negative in the first stripe: front padding), the XOR of the wave's lanes.  The loads of its
 // first batch into `a` were issued by crc_stripe_first, possibly before the tables were filled.
+// The stripe's raw CRC from its chains' registers after `m` groups folded, the XOR of the wave's lanes.
+// Horner over the chains in the order of their last groups: the chain whose last group is d groups before
+// the stripe's end is (m - 1 - d) mod kCrcChains; chains that took no group hold zero.  Then each lane's
+// register is shifted past the lanes after it.
+__device__ __forceinline__ uint32_t crc_stripe_close(const uint32_t* lds, const uint32_t* acc, int m,
+                                                     uint32_t lane_shift) {
+    const uint32_t* behind_table = lds;
+    uint32_t x = 0;
+#pragma unroll
+    for (int d = kCrcChains - 1; d >= 0; --d) {
+        const int c = ((m - 1 - d) % kCrcChains + kCrcChains) % kCrcChains;  // wave-uniform
+        uint32_t pick = acc[0];
+#pragma unroll
+        for (int k = 1; k < kCrcChains; ++k) pick = c == k ? acc[k] : pick;
+        x = (d == kCrcChains - 1 ? 0u : crc_advance(behind_table, x)) ^ pick;
+    }
+    // The lane's constant is the same for every job: hidden from the compiler here, or it keeps the
+    // multiply's 32 masks live across the job loop.
+    uint32_t shift = lane_shift;
+    asm volatile("" : "+v"(shift));
+    x = gf_mul(shift, x);
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) x ^= __shfl_xor(x, o);
+    return x;
+}
+
 template <bool kAligned>
 __device__ __forceinline__ uint32_t crc_stripe_rest(const uint32_t* lds, uint32_t lane, uint32_t cols,
                                                     uint32_t lane_shift, const uint8_t* __restrict__ rec,
                                                     int64_t start, int groups, u32x4* a) {
-    const uint32_t* behind_table = lds;
     const int lead = crc_lead(start);
     uint32_t acc[kCrcChains];
 #pragma unroll
@@ -789,27 +814,7 @@ __device__ __forceinline__ uint32_t crc_stripe_rest(const uint32_t* lds, uint32_
         crc_fold_batch(lds, cols, b, acc, kCrcChains);
         g += kCrcChains;
     }
-    // Horner over the chains in the order of their last groups: the chain whose last group is d groups
-    // before the stripe's end is (m - 1 - d) mod kCrcChains, m the groups folded; chains that took no
-    // group hold zero.
-    const int m = groups - lead;
-    uint32_t x = 0;
-#pragma unroll
-    for (int d = kCrcChains - 1; d >= 0; --d) {
-        const int c = ((m - 1 - d) % kCrcChains + kCrcChains) % kCrcChains;  // wave-uniform
-        uint32_t pick = acc[0];
-#pragma unroll
-        for (int k = 1; k < kCrcChains; ++k) pick = c == k ? acc[k] : pick;
-        x = (d == kCrcChains - 1 ? 0u : crc_advance(behind_table, x)) ^ pick;
-    }
-    // The lane's constant is the same for every job: hidden from the compiler here, or it keeps the
-    // multiply's 32 masks live across the job loop.
-    uint32_t shift = lane_shift;
-    asm volatile("" : "+v"(shift));
-    x = gf_mul(shift, x);
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) x ^= __shfl_xor(x, o);
-    return x;
+    return crc_stripe_close(lds, acc, groups - lead, lane_shift);
 }
 
 // x^(8 * stripe_bytes * 2^i) mod P: the shifts of a stripe past the ones after it.
@@ -874,6 +879,35 @@ __global__ __launch_bounds__(kCrcThreads) void crc_stripes_kernel(const uint8_t*
     }
 }
 
+// A round's stripe: its raw CRC shifted past the `behind` stripes after it in the record (stripes <= 16),
+// posted to the workgroup's LDS slot of wave `wave`.
+__device__ __forceinline__ void crc_stripe_post(uint32_t* stripe_crc, uint32_t lane, int wave, int behind,
+                                                const CrcStripePowers& powers, uint32_t x) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        if ((behind >> i) & 1) {
+            uint32_t power = powers.p[i];
+            asm volatile("" : "+s"(power));  // per round, as for the lane shift
+            x = gf_mul(power, x);
+        }
+    }
+    if (lane == 0) stripe_crc[wave] = x;
+}
+
+// The end of a round: once every wave has posted its stripe, one thread per record XORs the record's
+// stripes and adds the initial value's term.
+__device__ __forceinline__ void crc_round_combine(const uint32_t* stripe_crc, int stripes, int per_group,
+                                                  int64_t base, int64_t n_records, uint32_t init_term,
+                                                  uint32_t* __restrict__ out) {
+    __syncthreads();
+    if (threadIdx.x < static_cast<unsigned>(per_group) && base + threadIdx.x < n_records) {
+        uint32_t x = 0;
+        for (int k = 0; k < stripes; ++k) x ^= stripe_crc[threadIdx.x * stripes + k];
+        out[base + threadIdx.x] = ~(init_term ^ x);
+    }
+    __syncthreads();
+}
+
 // Whole records per workgroup: a round gives `per_group` records' stripes to
 // the workgroup's waves (wave w: record w / stripes, stripe w % stripes),
 // each wave shifts its stripe's raw CRC to the record's end, and the
@@ -897,25 +931,11 @@ __device__ __forceinline__ void crc_records_round(const uint32_t* lds, uint32_t*
         int64_t start = static_cast<int64_t>(j) * groups * kCrcGroup - static_cast<int64_t>(pad);
         asm volatile("" : "+s"(start));
         if (!loaded) crc_stripe_first<kAligned>(records + r * pitch, start, groups, lane, a);
-        uint32_t x = crc_stripe_rest<kAligned>(lds, lane, cols, lane_shift, records + r * pitch, start, groups, a);
-        const int behind = stripes - 1 - j;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {  // stripes <= 16
-            if ((behind >> i) & 1) {
-                uint32_t power = powers.p[i];
-                asm volatile("" : "+s"(power));  // per round, as for the lane shift
-                x = gf_mul(power, x);
-            }
-        }
-        if (lane == 0) stripe_crc[wave] = x;
+        const uint32_t x =
+            crc_stripe_rest<kAligned>(lds, lane, cols, lane_shift, records + r * pitch, start, groups, a);
+        crc_stripe_post(stripe_crc, lane, wave, stripes - 1 - j, powers, x);
     }
-    __syncthreads();
-    if (threadIdx.x < static_cast<unsigned>(per_group) && base + threadIdx.x < n_records) {
-        uint32_t x = 0;
-        for (int k = 0; k < stripes; ++k) x ^= stripe_crc[threadIdx.x * stripes + k];
-        out[base + threadIdx.x] = ~(init_term ^ x);
-    }
-    __syncthreads();
+    crc_round_combine(stripe_crc, stripes, per_group, base, n_records, init_term, out);
 }
 
 template <bool kAligned>
@@ -971,6 +991,163 @@ __global__ __launch_bounds__(256) void crc_combine_kernel(const uint32_t* __rest
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) x ^= __shfl_xor(x, o);
     if (lane == 0) out[r] = ~(init_term ^ x);
+}
+
+// ----------------------------------------------------------------- gather with CRC32C
+//
+// The save's gather into device records with every record's CRC32C folded in
+// on the way: one HBM pass (a read and a write of the session) where the
+// gather and the CRC32C kernel take two reads and a write.  It is the CRC32C
+// records kernel above with its loads taken from the cache and each word
+// written to its record once it has landed: the same stripes, chains, LDS
+// tables, batches and per-workgroup combine.  For layouts whose spans are
+// whole KiB (each 1 KiB group of a record lies in one span, so a wave's load
+// of a group is one 1 KiB run of the cache):
+//   group_bases[g] + block * group_pitches[g]   the source of record group g,
+// the groups' table built once per layout on the host.  A record's front
+// padding (the stripe plan's) is whole groups, which are skipped.
+
+using GlobalWord = const __attribute__((address_space(1))) u32x4;
+
+// The loads of the batch of record groups g, g + 1, ..., g + count - 1 (count >= 1) of `block` into v:
+// chains past `count` load the last of them again (crc_gather_zero then zeroes them).  The group's source
+// address is wave-uniform (scalar loads of the groups' table); lane l loads its 16 bytes.
+__device__ __forceinline__ void crc_gather_load(const int64_t* __restrict__ group_bases,
+                                                const int64_t* __restrict__ group_pitches, int64_t block, int g,
+                                                int count, uint32_t lane, u32x4* v) {
+#pragma unroll
+    for (int c = 0; c < kCrcChains; ++c) {
+        const int at = g + (c < count ? c : count - 1);
+        const uint64_t src = static_cast<uint64_t>(group_bases[at] + block * group_pitches[at]);
+        v[c] = __builtin_nontemporal_load(reinterpret_cast<GlobalWord*>(src + lane * kCrcRun));
+    }
+}
+
+__device__ __forceinline__ void crc_gather_zero(int count, u32x4* v) {
+#pragma unroll
+    for (int c = 1; c < kCrcChains; ++c)
+        if (c >= count) v[c] = u32x4{0u, 0u, 0u, 0u};  // wave-uniform
+}
+
+// The landed batch's words to the record (groups g .. g + count - 1 at `record`).  Ordinary stores: the
+// records are read again soon (the device-to-host copy, SHA-256), and a session of up to a few hundred MB
+// stays in the last-level cache between (nontemporal stores measured 4.7 against 5.7 TB/s at a TP = 8
+// shard's 151 MB, and 5.0 against 4.8 at 1.2 GB).
+__device__ __forceinline__ void crc_gather_store(char* __restrict__ record, int g, int count, uint32_t lane,
+                                                 const u32x4* v) {
+#pragma unroll
+    for (int c = 0; c < kCrcChains; ++c)
+        if (c < count)  // wave-uniform
+            *reinterpret_cast<u32x4*>(record + static_cast<int64_t>(g + c) * kCrcGroup + lane * kCrcRun) = v[c];
+}
+
+// One wave's job: record groups [g, end) of `block` gathered into `record` and folded; the first batch
+// was issued into `a` by crc_gather_load.  Returns the stripe's raw CRC (the XOR of the wave's lanes).
+__device__ __forceinline__ uint32_t crc_gather_stripe(const uint32_t* lds, uint32_t lane, uint32_t cols,
+                                                      uint32_t lane_shift, const int64_t* __restrict__ group_bases,
+                                                      const int64_t* __restrict__ group_pitches, int64_t block,
+                                                      char* __restrict__ record, int g, int end, u32x4* a) {
+    const int m = end - g;
+    uint32_t acc[kCrcChains];
+#pragma unroll
+    for (int c = 0; c < kCrcChains; ++c) acc[c] = 0;
+    u32x4 b[kCrcBatchWords];
+    int count = m < kCrcChains ? m : kCrcChains;
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // the first batch has landed (vmcnt(0))
+    crc_gather_zero(count, a);
+    while (true) {
+        if (g + 2 * kCrcChains > end) {
+            // a holds the last batch but one, or the last: store and fold it, then the rest (if any).
+            crc_gather_store(record, g, count, lane, a);
+            crc_fold_batch(lds, cols, a, acc, count);
+            g += kCrcChains;
+            if (g < end) {
+                count = end - g;
+                crc_gather_load(group_bases, group_pitches, block, g, count, lane, a);
+                crc_gather_zero(count, a);
+                crc_gather_store(record, g, count, lane, a);
+                crc_fold_batch(lds, cols, a, acc, count);
+            }
+            break;
+        }
+        crc_gather_load(group_bases, group_pitches, block, g + kCrcChains, kCrcChains, lane, b);
+        crc_gather_store(record, g, kCrcChains, lane, a);
+        crc_fold_batch(lds, cols, a, acc, kCrcChains);
+        g += kCrcChains;
+        count = kCrcChains;
+        if (g + 2 * kCrcChains > end) {
+            crc_gather_store(record, g, count, lane, b);
+            crc_fold_batch(lds, cols, b, acc, count);
+            g += kCrcChains;
+            if (g < end) {
+                count = end - g;
+                crc_gather_load(group_bases, group_pitches, block, g, count, lane, a);
+                crc_gather_zero(count, a);
+                crc_gather_store(record, g, count, lane, a);
+                crc_fold_batch(lds, cols, a, acc, count);
+            }
+            break;
+        }
+        crc_gather_load(group_bases, group_pitches, block, g + kCrcChains, kCrcChains, lane, a);
+        crc_gather_store(record, g, kCrcChains, lane, b);
+        crc_fold_batch(lds, cols, b, acc, kCrcChains);
+        g += kCrcChains;
+    }
+    return crc_stripe_close(lds, acc, m, lane_shift);
+}
+
+// Records `blocks` gathered to out + i * out_pitch, their CRC32C to crcs[i].  A record is `stripes` stripes
+// of `groups` groups, the first `lead` groups of stripe 0 being padding; the workgroup takes 16 / stripes
+// records a round (wave w: record w / stripes, stripe w % stripes), as crc_records_kernel does.
+__global__ __launch_bounds__(kCrcThreads) void gather_crc_kernel(
+    const int64_t* __restrict__ blocks, int64_t n_records, const int64_t* __restrict__ group_bases,
+    const int64_t* __restrict__ group_pitches, int stripes, int groups, int lead, CrcStripePowers powers,
+    uint32_t init_term, char* __restrict__ out, int64_t out_pitch, uint32_t* __restrict__ crcs) {
+    __shared__ uint32_t lds[(kCrcAdvanceBytes + kCrcPrivateBytes + kCrcBehindBytes) / 4];
+    __shared__ uint32_t stripe_crc[kCrcWaves];
+    const uint32_t lane = threadIdx.x & 63u;
+    const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
+    const int per_group = kCrcWaves / stripes;
+    const int rec_in_round = wave / stripes, j = wave - rec_in_round * stripes;
+    // The wave's record groups, the same every round.
+    const int g_begin = j == 0 ? 0 : j * groups - lead, g_end = (j + 1) * groups - lead;
+    const int64_t first = static_cast<int64_t>(blockIdx.x) * per_group;
+    const int64_t stride = static_cast<int64_t>(gridDim.x) * per_group;
+    uint32_t lane_shift, cols;
+    {
+        // Table words, then the first round's first batch (every wave: one without a record loads record
+        // 0's, so the compiler counts the loads as issued), in flight while the tables are filled.
+        const CrcTableWords words = crc_table_words();
+        lane_shift = g_crc_tables[kCrcLaneShift + lane];
+        const bool mine = rec_in_round < per_group && first + rec_in_round < n_records;  // wave-uniform
+        const int64_t r = mine ? first + rec_in_round : 0;
+        u32x4 a[kCrcBatchWords];
+        const int m = g_end - g_begin;
+        crc_gather_load(group_bases, group_pitches, blocks[r], g_begin, m < kCrcChains ? m : kCrcChains, lane, a);
+        crc_fill_tables(lds, words);
+        cols = crc_columns(lane);
+        crc_tables_ready();
+        if (mine) {
+            const uint32_t x = crc_gather_stripe(lds, lane, cols, lane_shift, group_bases, group_pitches, blocks[r],
+                                                 out + r * out_pitch, g_begin, g_end, a);
+            crc_stripe_post(stripe_crc, lane, wave, stripes - 1 - j, powers, x);
+        }
+        if (first < n_records)  // workgroup-uniform
+            crc_round_combine(stripe_crc, stripes, per_group, first, n_records, init_term, crcs);
+    }
+    for (int64_t base = first + stride; base < n_records; base += stride) {
+        const int64_t r = base + rec_in_round;
+        if (rec_in_round < per_group && r < n_records) {  // wave-uniform
+            const int m = g_end - g_begin;
+            u32x4 a[kCrcBatchWords];
+            crc_gather_load(group_bases, group_pitches, blocks[r], g_begin, m < kCrcChains ? m : kCrcChains, lane,
+                            a);
+            const uint32_t x = crc_gather_stripe(lds, lane, cols, lane_shift, group_bases, group_pitches, blocks[r],
+                                                 out + r * out_pitch, g_begin, g_end, a);
+            crc_stripe_post(stripe_crc, lane, wave, stripes - 1 - j, powers, x);
+        }
+        crc_round_combine(stripe_crc, stripes, per_group, base, n_records, init_term, crcs);
+    }
 }
 
 // ----------------------------------------------------------------- restore with CRC32C
@@ -2086,6 +2263,40 @@ int kvsnap_gather_blocks_checked(const int64_t* dests, const int64_t* blocks, in
                                lds, s, dests, blocks, n_blocks, span_offsets, span_bases, span_pitches, span_words,
                                n_spans, stage_at, pitch, partial);
         check_launch("checked gather");
+    });
+}
+
+int kvsnap_gather_crc32c_fits(uint64_t record_bytes) {
+    return record_bytes > 0 && record_bytes % kCrcGroup == 0 && record_bytes < (uint64_t(1) << 31) ? 1 : 0;
+}
+
+int kvsnap_gather_crc32c(const int64_t* blocks, int64_t n_blocks, const int64_t* group_bases,
+                         const int64_t* group_pitches, uint64_t record_bytes, void* out, int64_t out_pitch,
+                         uint32_t* crcs, uintptr_t stream) {
+    return guard([&] {
+        if (n_blocks < 0) throw std::runtime_error("negative gather size");
+        if (n_blocks == 0) return;
+        if (!kvsnap_gather_crc32c_fits(record_bytes))
+            throw std::runtime_error("gather with CRC32C: records must be whole KiB, under 2 GiB");
+        if (!blocks || !group_bases || !group_pitches || !out || !crcs)
+            throw std::runtime_error("gather with CRC32C: tables, records and CRC32Cs must be device pointers");
+        if (reinterpret_cast<uintptr_t>(out) % 16 || out_pitch % 16 || static_cast<uint64_t>(out_pitch) < record_bytes)
+            throw std::runtime_error("gather with CRC32C: records must be 16-byte aligned and not overlap");
+        if (reinterpret_cast<uintptr_t>(crcs) % 4) throw std::runtime_error("gather with CRC32C: CRC32Cs misaligned");
+        ensure_crc_tables();
+        // At most 16 stripes a record, so a workgroup's 16 waves hold whole records.
+        const CrcPlan plan = crc_plan(record_bytes, n_blocks, int64_t(kCrcWaves) * n_blocks);
+        const int stripes = static_cast<int>(plan.stripes);
+        const int64_t per_group = kCrcWaves / stripes;
+        CrcStripePowers powers;
+        const uint64_t stripe_bytes = static_cast<uint64_t>(plan.groups) * kCrcGroup;
+        for (int i = 0; i < 6; ++i) powers.p[i] = host_xpow8n(stripe_bytes << i);
+        const unsigned grid = grid_for((n_blocks + per_group - 1) / per_group, kCrcGrid);
+        hipLaunchKernelGGL(gather_crc_kernel, dim3(grid), dim3(kCrcThreads), 0, reinterpret_cast<hipStream_t>(stream),
+                           blocks, n_blocks, group_bases, group_pitches, stripes, plan.groups,
+                           static_cast<int>(plan.pad / kCrcGroup), powers, host_shift(~0u, record_bytes),
+                           static_cast<char*>(out), out_pitch, crcs);
+        check_launch("gather with CRC32C");
     });
 }
 

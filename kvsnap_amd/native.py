@@ -45,6 +45,8 @@ KERNEL_SIGNATURES = {
     "kvsnap_restore_blocks": "int <- ptr ptr i64 ptr ptr ptr ptr i64 i64 int stream",
     "kvsnap_restore_blocks_checked": "int <- ptr ptr i64 ptr ptr ptr ptr i64 int ptr stream",
     "kvsnap_gather_blocks_checked": "int <- ptr ptr i64 ptr ptr ptr ptr i64 ptr i64 int ptr stream",
+    "kvsnap_gather_crc32c_fits": "int <- u64",
+    "kvsnap_gather_crc32c": "int <- ptr i64 ptr ptr u64 ptr i64 ptr stream",
     "kvsnap_restore_checked_crc32c": "int <- ptr i64 ptr ptr i64 u64 ptr stream",
     "kvsnap_gather_blocks": "int <- ptr i64 ptr ptr ptr ptr i64 i64 ptr i64 int stream",
     "kvsnap_scatter_blocks": "int <- ptr i64 ptr i64 ptr ptr ptr ptr i64 i64 int stream",

@@ -110,6 +110,26 @@ class HostKernels:
             C.c_uint32.from_address(partial + 4 * i * n_spans).value = oracle.crc32c(C.string_at(dest, record_bytes))
         return 0
 
+    #: Whether kvsnap_gather_crc32c_fits admits whole-KiB records: off, so hashed saves gather and then take
+    #: their CRC32Cs, unless a test turns it on.
+    fused = False
+
+    def kvsnap_gather_crc32c_fits(self, record_bytes):
+        return int(self.fused and record_bytes % 1024 == 0)
+
+    def kvsnap_gather_crc32c(self, blocks, n, group_bases, group_pitches, record_bytes, out, out_pitch, crcs,
+                             stream):
+        """The gather with CRC32C: each record from its 1 KiB groups' sources, and its CRC32C."""
+        self.launches.append(("gather_crc", n))
+        groups = record_bytes // 1024
+        bases, pitches = self._int64(group_bases, groups), self._int64(group_pitches, groups)
+        for i, block in enumerate(self._int64(blocks, n)):
+            for g in range(groups):
+                C.memmove(out + i * out_pitch + 1024 * g, bases[g] + block * pitches[g], 1024)
+            C.c_uint32.from_address(crcs + 4 * i).value = oracle.crc32c(C.string_at(out + i * out_pitch,
+                                                                                    record_bytes))
+        return 0
+
     def kvsnap_crc32c_workspace_bytes(self, record_bytes, n):
         return 16
 
@@ -278,6 +298,7 @@ def host_kernels():
     kernels = HostKernels()
     with patch.object(dataplane, "kernel_library", lambda library=None: kernels), \
          patch.object(dataplane, "_int64_device_tensors", host_tables), \
+         patch.object(dataplane, "_int32_device_output", lambda t, device, count: None), \
          patch.object(dataplane, "_current_stream_handle", lambda device: 0):
         yield kernels
 
@@ -1054,3 +1075,77 @@ def test_a_hashed_direct_save_gathers_records_stage_and_crcs_in_one_pass(host_ke
         want[(tokens % TOKENS) * HEADS * WIDTH * 2:] = bytes(len(want) - (tokens % TOKENS) * HEADS * WIDTH * 2)
         assert pinned[2 * size:2 * size + SPAN] == bytes(want)
         assert ("crc32c", 1) in host_kernels.launches
+
+
+@pytest.mark.parametrize("tokens", [3 * TOKENS, 3 * TOKENS - 5])
+@pytest.mark.parametrize("limit,fused", [(1 << 30, True), (0, False)])
+def test_a_small_hashed_staged_save_gathers_records_and_crcs_in_one_pass(host_kernels, monkeypatch, tokens, limit,
+                                                                        fused):
+    """A staged save with digests of at most GATHER_CRC_MAX_BYTES, over whole-KiB spans: one gather with CRC32C
+    packs the device records (the copies' and the SHA-256 kernels' input) and gives their CRC32Cs, and the hash
+    job gets them and launches only the SHA-256.  A zeroed tail has its record's CRC32C taken again.  Over the
+    limit the save gathers and leaves the CRC32Cs to the hash job.  Either way the pinned records equal the
+    device records, and every given CRC32C the oracle's over its pinned record."""
+    monkeypatch.setattr(dataplane, "GATHER_CRC_MAX_BYTES", limit)
+    host_kernels.fused = True
+    caches = qwen3_8b_caches(6, seed=5)
+    plane = plane_over(caches)
+    size = plane.block_bytes
+    seen = {}
+
+    class Job:
+        def __init__(self, torch_module, records_ptr, record_bytes, record_pitch, n, device, lane, slice_blocks, *,
+                     timer=None, keepalive=None, crc=None):
+            seen.update(records=C.string_at(records_ptr, n * record_bytes), crc=crc)
+            self.crc = crc
+            self.sha = torch.zeros((n, 32), dtype=torch.uint8)
+
+        def query(self):
+            return True
+
+        def finished(self, timeout=None):
+            return True
+
+        def synchronize(self):
+            pass
+
+    targets = slabs(plane, 3, shared=True)
+    with patch.object(dataplane, "HashJob", Job), \
+         patch.object(TorchBlockDataPlane, "_hash_lane", lambda self: MagicMock()):
+        plane.save_gather([5, 2, 4], targets, tokens, digests=[])
+    kinds = [kind for kind, _ in host_kernels.launches]
+    assert [k for k in kinds if k.startswith("gather")] == (["gather_crc"] if fused else ["gather"])
+    pinned = targets[0][0].at(0, 3 * size)
+    assert seen["records"] == pinned
+    for i, block in enumerate([5, 2, 4]):
+        for position, name in enumerate(sorted(caches)):
+            want = bytearray(span_of(caches[name], block))
+            if i == 2 and tokens % TOKENS:
+                cut = (tokens % TOKENS) * HEADS * WIDTH * 2
+                want[cut:] = bytes(len(want) - cut)
+            assert pinned[i * size + position * SPAN:i * size + (position + 1) * SPAN] == bytes(want), (block, name)
+    if fused:
+        crcs = [int(c) & 0xFFFFFFFF for c in seen["crc"].view(torch.int32).tolist()]
+        assert crcs == [oracle.crc32c(pinned[i * size:(i + 1) * size]) for i in range(3)]
+        assert kinds.count("crc32c") == (1 if tokens % TOKENS else 0)   # the zeroed tail's record, taken again
+    else:
+        assert seen["crc"] is None and "crc32c" not in kinds
+
+
+def test_the_groups_table_follows_the_spans_and_is_refused_for_spans_that_are_not_whole_kib(host_kernels):
+    """For whole-KiB spans, group g of a record comes from its span's base plus (g's KiB within the span), at the
+    span's pitch; a layout with a span of another length has no table (its saves gather, then take CRC32Cs)."""
+    host_kernels.fused = True
+    caches = qwen3_8b_caches(4, seed=1)
+    plane = plane_over(caches)
+    bases, pitches = plane.group_tables()
+    spans = plane.spans()
+    assert bases.numel() == pitches.numel() == plane.block_bytes // 1024
+    for offset, base, pitch, nbytes in spans:
+        for k in range(nbytes // 1024):
+            assert (int(bases[offset // 1024 + k]), int(pitches[offset // 1024 + k])) == (base + 1024 * k, pitch)
+    storage = torch.zeros((2, 4, 16, 1, 40), dtype=torch.bfloat16)          # 1280-byte spans
+    odd = plane_over({f"model.layers.{i}.self_attn.attn": storage[i].permute(0, 2, 1, 3) for i in range(2)})
+    assert odd.group_tables() is None
+    host_kernels.fused = False
+    assert plane_over(caches).group_tables() is None

@@ -14,7 +14,8 @@ import pytest
 torch = pytest.importorskip("torch")
 
 from kvsnap_amd import synth
-from kvsnap_amd.dataplane import TorchBlockDataPlane, _check, digest_device_records, kernel_library
+from kvsnap_amd.dataplane import (TorchBlockDataPlane, _check, digest_device_records, gather_crc32c_launcher,
+                                  kernel_library)
 
 pytestmark = pytest.mark.gpu
 
@@ -872,6 +873,45 @@ def test_the_checked_gather_kernel_gives_the_oracle_s_records_and_crc32cs(
     if with_stage:
         assert np.array_equal(stage.cpu().numpy().reshape(n, size), expected)
     assert [value & 0xFFFFFFFF for value in out.tolist()] == [oracle_lib.crc32c(r.tobytes()) for r in expected]
+    assert np.array_equal(host_copy(backing), before)
+
+
+@pytest.mark.parametrize("layers,layout,heads,head_dim,blocks_total,n,gap", [
+    (4, "vllm", 8, 128, 64, 29, 0),         # 64 KiB spans: 256-group records
+    (4, "kv_split", 8, 128, 64, 29, 1024),  # 32 KiB spans, records 1 KiB apart past their ends
+    (36, "kv_split", 1, 128, 64, 29, 0),    # a TP = 8 shard of Qwen3-8B: 72 spans of 4 KiB, 288 groups
+    (36, "vllm", 1, 128, 64, 3, 0),         # 3 records: most of the grid's waves have none
+    (17, "vllm", 1, 16, 5200, 5000, 0),     # 17-group records: a padded first stripe, short batches, two rounds
+])
+def test_the_gather_with_crc32c_gives_the_oracle_s_records_and_crc32cs(planes, oracle_lib, layers, layout, heads,
+                                                                       head_dim, blocks_total, n, gap):
+    """kvsnap_gather_crc32c through the C-ABI over the plane's groups' table: every device record equals the
+    oracle's gather of its block and every CRC32C the oracle's (csrc/dataplane/io.cpp:39-44), for stripe plans
+    with and without front padding, partial batches, idle waves and more records than one round; the cache is
+    only read and nothing past a record is written."""
+    caches, backing = synth.make_caches(layers, blocks_total, block_size=16, heads=heads, head_dim=head_dim,
+                                        layout=layout)
+    raw = backing.view(torch.uint8)
+    generator = torch.Generator(device="cuda").manual_seed(25)
+    raw.copy_(torch.randint(0, 256, raw.shape, dtype=torch.uint8, device="cuda", generator=generator))
+    plane = planes(caches, block_size=16)
+    size = plane.block_bytes
+    pitch = size + gap
+    blocks = random.Random(27).sample(range(blocks_total), n)
+    before = host_copy(backing)
+    expected = oracle_lib.gather(host_spans(plane, backing, before), blocks, size)
+    groups = plane.group_tables()
+    assert groups is not None and groups[0].numel() == size // 1024
+    out = torch.full((n * pitch,), 0xA5, dtype=torch.uint8, device="cuda")
+    crcs = torch.zeros(n, dtype=torch.int32, device="cuda")
+    ids = torch.tensor(blocks, dtype=torch.int64, device="cuda")
+    print(f"gather with CRC32C: {layers} layers {layout}, {size} B records, n={n}, pitch={pitch}", flush=True)
+    gather_crc32c_launcher(ids, *groups, size, out.data_ptr(), pitch, crcs)()
+    torch.cuda.synchronize()
+    written = out.cpu().numpy().reshape(n, pitch)
+    assert np.array_equal(written[:, :size], expected)
+    assert (written[:, size:] == 0xA5).all()
+    assert [value & 0xFFFFFFFF for value in crcs.tolist()] == [oracle_lib.crc32c(r.tobytes()) for r in expected]
     assert np.array_equal(host_copy(backing), before)
 
 

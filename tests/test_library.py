@@ -64,3 +64,11 @@ def test_missing_hip_library_fails_loudly(monkeypatch, tmp_path):
     monkeypatch.setenv("KVSNAP_CUDA_LIBRARY", str(tmp_path / "absent.so"))
     with pytest.raises(RuntimeError, match="not built"):
         dataplane.kernel_library()
+
+
+def test_the_gather_with_crc32c_takes_whole_kib_records_under_2_gib_only():
+    """kvsnap_gather_crc32c_fits (host logic only): whole KiB, more than none, under 2 GiB."""
+    hip = C.CDLL(str(HIP_LIBRARY))
+    hip.kvsnap_gather_crc32c_fits.argtypes = [C.c_uint64]
+    assert [hip.kvsnap_gather_crc32c_fits(n) for n in (1024, 2359296, 294912, (1 << 31) - 1024)] == [1, 1, 1, 1]
+    assert [hip.kvsnap_gather_crc32c_fits(n) for n in (0, 16, 1280, 2359296 + 16, 1 << 31, 1 << 40)] == [0] * 6
