@@ -68,14 +68,15 @@ PCIE5_X16_GBPS = round(32 * 16 * 128 / 130 / 8, 2)
 # The round wave issues 596 VALU per 64-byte block (counted in the gfx950 ISA
 # of sha256_kernel: 192 alignbit, 192 bitop3, 74 DPP adds, 64 add3, 64 xad,
 # 10 others); a wave64 VALU takes 4 cycles of its SIMD at the 2.4 GHz peak
-# engine clock (the kernel's own clock counters read 2.39-2.40 GHz).  All
-# chains run side by side (one round wave per 32 records).  Timed alone on
-# one wave, a round's own 9-VALU sequence takes 37.5 cycles: the bound at that
-# rate is reported beside the nominal one.
+# engine clock.  All chains run side by side (one round wave per 32 records).
+# The round's own 9-VALU sequence is also timed live on one wave
+# (kvsnap_sha_round_probe: shader cycles and the 100 MHz constant clock), which
+# gives the rate a slot runs at and the engine clock meanwhile; the bound at
+# that rate is reported beside the nominal one.
 SHA_VALU_PER_BLOCK = 596
 SHA_CYCLES_PER_VALU = 4
-SHA_ROUND_CYCLES = 37.5
 ENGINE_CLOCK_GHZ = 2.4
+SHA_PROBE_SLOTS = 1 << 18
 # A floor that does not come from the kernel: FIPS 180-4's round in gfx950
 # instructions.  A round is six 32-bit additions (T1 = h + Sigma1 + Ch + (W+K),
 # e = d + T1, T2 = Sigma0 + Maj, a = T1 + T2; W+K comes summed from the message
@@ -92,12 +93,31 @@ SHA_FIPS_TWO_LANE_ROUND = (SHA_FIPS_ROUND_INSTRUCTIONS + 1) // 2 + 1
 SHA_FIPS_FEED_FORWARD = 4
 
 
-def sha_issue_bound(record_bytes, records, ms):
-    """Fraction of the per-chain VALU issue bound the SHA-256 kernel reached."""
+def sha_round_rate(torch):
+    """The SHA-256 round sequence timed on one wave (median of 5): shader cycles a slot and the engine clock in
+    GHz (cycles over the 100 MHz constant clock's ticks)."""
+    from kvsnap_amd.dataplane import _check, kernel_library
+    lib = kernel_library()
+    out = torch.zeros(3, dtype=torch.int64, device="cuda")
+    stream = torch.cuda.current_stream()
+    samples = []
+    for seed in range(6):
+        _check(lib, lib.kvsnap_sha_round_probe(seed, SHA_PROBE_SLOTS, out.data_ptr(), stream.cuda_stream))
+        cycles, ticks, _ = out.tolist()
+        if seed:                       # the first launch warms the clock up
+            samples.append((cycles / SHA_PROBE_SLOTS, cycles / (ticks * 10.0)))
+    samples.sort()
+    return samples[len(samples) // 2]
+
+
+def sha_issue_bound(record_bytes, records, ms, round_rate):
+    """Fraction of the per-chain VALU issue bound the SHA-256 kernel reached; ``round_rate`` is
+    sha_round_rate's (cycles a slot, engine GHz)."""
     blocks = record_bytes // 64 + (1 if record_bytes % 64 + 9 <= 64 else 2)
     bound_ms = blocks * SHA_VALU_PER_BLOCK * SHA_CYCLES_PER_VALU / (ENGINE_CLOCK_GHZ * 1e6)
     total = record_bytes * records
-    sequence_ms = blocks * 64 * SHA_ROUND_CYCLES / (ENGINE_CLOCK_GHZ * 1e6)
+    slot_cycles, clock_ghz = round_rate
+    sequence_ms = blocks * 64 * slot_cycles / (ENGINE_CLOCK_GHZ * 1e6)
     fips_ms = blocks * (64 * SHA_FIPS_TWO_LANE_ROUND + SHA_FIPS_FEED_FORWARD) * SHA_CYCLES_PER_VALU / (
         ENGINE_CLOCK_GHZ * 1e6)
     one_lane_ms = blocks * (64 * SHA_FIPS_ROUND_INSTRUCTIONS + 2 * SHA_FIPS_FEED_FORWARD) * SHA_CYCLES_PER_VALU / (
@@ -110,7 +130,9 @@ def sha_issue_bound(record_bytes, records, ms):
                            "source": "FIPS 180-4 round operations in gfx950 instructions (add3, alignbit, bitop3)"},
             "cycles_per_valu": SHA_CYCLES_PER_VALU, "clock_ghz": ENGINE_CLOCK_GHZ, "bound_ms": round(bound_ms, 3),
             "achieved": round(total / (ms * 1e6), 2), "peak": round(total / (bound_ms * 1e6), 2), "unit": "GB/s",
-            "frac": round(bound_ms / ms, 4), "round_cycles_measured": SHA_ROUND_CYCLES,
+            "frac": round(bound_ms / ms, 4), "round_cycles_measured": round(slot_cycles, 2),
+            "round_probe_clock_ghz": round(clock_ghz, 3),
+            "round_probe": "kvsnap_sha_round_probe: the round sequence alone on one wave, s_memtime / s_memrealtime",
             "round_sequence_bound_ms": round(sequence_ms, 3), "frac_of_round_sequence_rate": round(sequence_ms / ms, 4)}
 
 
@@ -551,7 +573,7 @@ def run_save_restore(args):
         "sha256": {"kernel": "sha256_kernel", "ms": round(sha_alone_ms, 3),
                    "gbps": round(total / (sha_alone_ms * 1e6), 2), "records": session,
                    "in_step_ms": round(sha["avg_ms"], 3),
-                   "issue_roofline": sha_issue_bound(size, session, sha_alone_ms),
+                   "issue_roofline": sha_issue_bound(size, session, sha_alone_ms, sha_round_rate(torch)),
                    "cpu_ms_by_threads": cpu["legs_ms"]["sha256"] if cpu else None},
         "parity": {"restore_byte_exact": exact, "digests_bit_exact": digests_exact},
         "cpu_baseline": cpu,
@@ -1096,7 +1118,8 @@ def run_kernels(args):
         ms = median_ms(torch, stream, fn, reps=reps, batch=1 if name == "sha256_kernel" else 4)
         out[name] = {"ms": round(ms, 4), "algorithmic_bytes": algorithmic,
                      "gbps": round(algorithmic / ms / 1e6, 1)}
-    out["sha256_kernel"]["issue_roofline"] = sha_issue_bound(size, session, out["sha256_kernel"]["ms"])
+    out["sha256_kernel"]["issue_roofline"] = sha_issue_bound(size, session, out["sha256_kernel"]["ms"],
+                                                          sha_round_rate(torch))
     # The checked gather's CRC32Cs against the CRC kernel's over the same records (the last run of each).
     runs["crc_records_kernel"][0]()
     want = crc.clone()

@@ -219,6 +219,13 @@ int kvsnap_sha256_ranges(int count, const uint64_t* records, const uint64_t* rec
                          const uint64_t* record_pitches, const int64_t* n_records, const uint64_t* first_blocks,
                          const uint64_t* end_blocks, const uint64_t* states, const uint64_t* outs, uintptr_t stream);
 
+/* The SHA-256 round's own issue rate, measured on the GPU: one wave runs
+ * `reps` (a multiple of 16) slots of sha256_kernel's round sequence with no
+ * memory traffic, and out (3 device words) receives the shader-clock cycles,
+ * the 100 MHz constant-clock ticks and a checksum.  No reference
+ * counterpart: the bench's SHA-256 bound is priced from it. */
+int kvsnap_sha_round_probe(uint32_t seed, int reps, uint64_t* out, uintptr_t stream);
+
 /* Streams of the data plane's own (no reference counterpart; the reference
  * copies on one stream).  kvsnap_stream_create makes a non-blocking stream of
  * default priority on `device`; kvsnap_stream_destroy waits for its work and

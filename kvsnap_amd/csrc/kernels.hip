@@ -1884,6 +1884,50 @@ __global__ __launch_bounds__(kShaThreads) void sha256_ranges_kernel(ShaRanges ra
                            blockIdx.x);
 }
 
+// The round's own issue rate, measured: one wave runs `reps` slots of the
+// round waves' instruction sequence (sha_slot, both halves) on values seeded
+// per lane, with no LDS, no waits and no barrier, between two reads of the
+// shader clock (s_memtime) and of the 100 MHz constant clock (s_memrealtime).
+// out[0] = shader cycles, out[1] = constant-clock ticks, out[2] = a checksum
+// of the lanes' state (so the slots are not optimised away).
+constexpr int kShaProbeUnroll = 16;
+
+__global__ __launch_bounds__(64) void sha_round_probe_kernel(uint32_t seed, int reps, uint64_t* __restrict__ out) {
+    const int lane = threadIdx.x;
+    const bool a_lane = (lane >> 2) & 1;
+    ShaHalf half = a_lane ? ShaHalf{2, 13, 22, ~0u} : ShaHalf{6, 11, 25, 0u};
+    opaque(half.m);
+    ShaLanes l;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        l.x[i] = seed * 0x9E3779B9u + static_cast<uint32_t>(lane * 4 + i) * 0x85EBCA6Bu;
+        l.e[i] = l.f[i] = 0;
+    }
+    uint32_t word = a_lane ? 1u : seed ^ 0x5A827999u;
+    opaque(word);
+    const int rounds = reps / kShaProbeUnroll;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) opaque(l.x[i]);
+    const uint64_t c0 = __builtin_amdgcn_s_memtime();
+    const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
+    for (int r = 0; r < rounds; ++r) {
+#pragma unroll
+        for (int k = 0; k < kShaProbeUnroll; ++k) sha_slot(l, word, half);
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) opaque(l.x[i]);
+    const uint64_t c1 = __builtin_amdgcn_s_memtime();
+    const uint64_t t1 = __builtin_amdgcn_s_memrealtime();
+    uint32_t sum = l.x[0] ^ l.x[1] ^ l.x[2] ^ l.x[3];
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) sum ^= __shfl_xor(sum, o);
+    if (lane == 0) {
+        out[0] = c1 - c0;
+        out[1] = t1 - t0;
+        out[2] = sum;
+    }
+}
+
 // ----------------------------------------------------------------- host helpers
 
 uint32_t host_gf_mul(uint32_t a, uint32_t b) {
@@ -2597,6 +2641,17 @@ int kvsnap_sha256_records(const void* records, uint64_t record_bytes, uint64_t r
                           uint8_t* out, uintptr_t stream) {
     return kvsnap_sha256_records_range(records, record_bytes, record_pitch, n_records, 0,
                                        kvsnap_sha256_blocks(record_bytes), nullptr, out, stream);
+}
+
+int kvsnap_sha_round_probe(uint32_t seed, int reps, uint64_t* out, uintptr_t stream) {
+    return guard([&] {
+        if (reps < kShaProbeUnroll || reps % kShaProbeUnroll || reps > (1 << 24))
+            throw std::runtime_error("SHA-256 round probe: reps a multiple of 16, at most 2^24");
+        if (!out || reinterpret_cast<uintptr_t>(out) % 8) throw std::runtime_error("SHA-256 round probe: bad output");
+        hipLaunchKernelGGL(sha_round_probe_kernel, dim3(1), dim3(64), 0, reinterpret_cast<hipStream_t>(stream), seed,
+                           reps, out);
+        check_launch("SHA-256 round probe");
+    });
 }
 
 int kvsnap_stream_create(int device, uintptr_t* stream) {

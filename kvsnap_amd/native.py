@@ -63,6 +63,7 @@ KERNEL_SIGNATURES = {
     "kvsnap_sha256_blocks": "u64 <- u64",
     "kvsnap_sha256_records_range": "int <- ptr u64 u64 i64 u64 u64 ptr ptr stream",
     "kvsnap_sha256_ranges": "int <- int ptr ptr ptr ptr ptr ptr ptr ptr stream",
+    "kvsnap_sha_round_probe": "int <- u32 int ptr stream",
     "kvsnap_stream_create": "int <- int size*",
     "kvsnap_stream_destroy": "int <- stream",
     "kvsnap_hold_stream": "int <- stream int",

@@ -1228,3 +1228,22 @@ def test_pipelined_disk_restore_is_byte_exact_and_refuses_corrupt_blobs(planes, 
     with pytest.raises(CorruptSnapshotError):
         plane.load_from_disk(restored, store, segments, chunk_bytes=6 * size, workers=3, verify=verify)
     staged.close()
+
+
+def test_the_sha_round_probe_times_the_round_sequence(hip_library):
+    """kvsnap_sha_round_probe: the round sequence on one wave takes at least its 9 VALU at 4 cycles each a slot
+    (and not wildly more), the engine clock it reports is a plausible MI355X clock, and the slots were run (the
+    checksum depends on the seed)."""
+    out = torch.zeros(3, dtype=torch.int64, device="cuda")
+    stream = torch.cuda.current_stream().cuda_stream
+    lib = kernel_library()
+    sums = []
+    for seed in (1, 2):
+        _check(lib, lib.kvsnap_sha_round_probe(seed, 1 << 16, out.data_ptr(), stream))
+        cycles, ticks, checksum = out.tolist()
+        sums.append(checksum)
+    slot = cycles / (1 << 16)
+    ghz = cycles / (ticks * 10.0)
+    assert 36 <= slot < 60, slot
+    assert 0.8 < ghz < 2.6, ghz
+    assert sums[0] != sums[1]

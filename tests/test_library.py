@@ -72,3 +72,13 @@ def test_the_gather_with_crc32c_takes_whole_kib_records_under_2_gib_only():
     hip.kvsnap_gather_crc32c_fits.argtypes = [C.c_uint64]
     assert [hip.kvsnap_gather_crc32c_fits(n) for n in (1024, 2359296, 294912, (1 << 31) - 1024)] == [1, 1, 1, 1]
     assert [hip.kvsnap_gather_crc32c_fits(n) for n in (0, 16, 1280, 2359296 + 16, 1 << 31, 1 << 40)] == [0] * 6
+
+
+def test_the_sha_round_probe_refuses_a_bad_count_before_any_gpu_call():
+    """kvsnap_sha_round_probe checks its arguments on the host first (no GPU here)."""
+    hip = C.CDLL(str(HIP_LIBRARY))
+    hip.kvsnap_sha_round_probe.argtypes = [C.c_uint32, C.c_int, C.c_void_p, C.c_size_t]
+    hip.kvsnap_cuda_error.restype = C.c_char_p
+    for reps in (0, 15, 17, (1 << 24) + 16):
+        assert hip.kvsnap_sha_round_probe(0, reps, 8, 0) == -1
+        assert b"multiple of 16" in hip.kvsnap_cuda_error()
