@@ -1063,42 +1063,67 @@ def run_kernels(args):
     source, target = synth.block_tables(num_blocks, session)
     tables = plane._load_tables()
     stream = torch.cuda.current_stream()
-    ids = torch.tensor(source, dtype=torch.int64, device="cuda")
-    stage = torch.empty(total, dtype=torch.uint8, device="cuda")
-    other = torch.empty(total, dtype=torch.uint8, device="cuda")
+    # With --rotate N the HBM kernels cycle over N sets of blocks and buffers, so that no launch finds the bytes
+    # of the launch before it in the last-level cache (a TP = 8 shard's 151 MB would otherwise stay there).
+    rot = max(1, args.rotate)
+    used = set(source) | set(target)
+    spare = [b for b in range(num_blocks) if b not in used]
+    extra = random.Random(11).sample(spare, 2 * (rot - 1) * session) if rot > 1 else []
+    sources = [source] + [extra[2 * k * session:(2 * k + 1) * session] for k in range(rot - 1)]
+    targets_ = [target] + [extra[(2 * k + 1) * session:(2 * k + 2) * session] for k in range(rot - 1)]
+    id_sets = [torch.tensor(x, dtype=torch.int64, device="cuda") for x in sources]
+    dst_sets = [torch.tensor(x, dtype=torch.int64, device="cuda") for x in targets_]
+    stages = [torch.empty(total, dtype=torch.uint8, device="cuda") for _ in range(rot)]
+    others = [torch.empty(total, dtype=torch.uint8, device="cuda") for _ in range(rot)]
+    ids, stage, dst = id_sets[0], stages[0], dst_sets[0]
     staged = plane.pool.reserve(total)
     pinned = torch.tensor([staged.pointer + i * size for i in range(session)], dtype=torch.int64, device="cuda")
-    dst = torch.tensor(target, dtype=torch.int64, device="cuda")
     lib = kernel_library()
     crc = torch.empty(session, dtype=torch.int32, device="cuda")
     work_bytes = int(lib.kvsnap_crc32c_workspace_bytes(size, session))
     work = torch.empty(work_bytes, dtype=torch.uint8, device="cuda")
     sha = torch.empty((session, 32), dtype=torch.uint8, device="cuda")
     hint = plane.min_span_bytes
-    records_at = torch.tensor([stage.data_ptr() + i * size for i in range(session)], dtype=torch.int64, device="cuda")
+    records_at = [torch.tensor([st.data_ptr() + i * size for i in range(session)], dtype=torch.int64, device="cuda")
+                  for st in stages]
     partial = torch.empty(session * tables[0].numel(), dtype=torch.int32, device="cuda")
+
+    def cycling(launch):
+        """launch(k) on set 0, 1, ..., rot - 1, 0, ... in turn, and launch itself for set k."""
+        turn = [0]
+
+        def next_set():
+            k, turn[0] = turn[0], (turn[0] + 1) % rot
+            return launch(k)
+        next_set.on = launch
+        return next_set
+
+    def gather_checked(k):
+        _check(lib, lib.kvsnap_gather_blocks_checked(
+            records_at[k].data_ptr(), id_sets[k].data_ptr(), session, *(t.data_ptr() for t in tables),
+            tables[0].numel(), None, 0, 0, partial.data_ptr(), stream.cuda_stream))
+        _check(lib, lib.kvsnap_restore_checked_crc32c(partial.data_ptr(), session, tables[0].data_ptr(),
+                                                      tables[3].data_ptr(), tables[0].numel(), size, crc.data_ptr(),
+                                                      stream.cuda_stream))
+
     runs = {
-        "plain_copy": (lambda: other.copy_(stage), 2 * total, args.reps),
-        "gather_pieces_kernel": (lambda: gather_blocks(ids, *tables, stage.data_ptr(), size, min_span_bytes=hint),
-                                 2 * total, args.reps),
+        "plain_copy": (cycling(lambda k: others[k].copy_(stages[k])), 2 * total, args.reps),
+        "gather_pieces_kernel": (cycling(lambda k: gather_blocks(id_sets[k], *tables, stages[k].data_ptr(), size,
+                                                                 min_span_bytes=hint)), 2 * total, args.reps),
         # 512 records take the one-launch plan (crc_records_kernel: stripes combined in the workgroup).
-        "crc_records_kernel": (lambda: _check(lib, lib.kvsnap_crc32c_records(
-            stage.data_ptr(), size, size, session, 0, crc.data_ptr(), work.data_ptr(), work_bytes,
-            stream.cuda_stream)), total, args.reps),
+        "crc_records_kernel": (cycling(lambda k: _check(lib, lib.kvsnap_crc32c_records(
+            stages[k].data_ptr(), size, size, session, 0, crc.data_ptr(), work.data_ptr(), work_bytes,
+            stream.cuda_stream))), total, args.reps),
         "restore_kernel": (lambda: copy_host_blocks(pinned, dst, *tables, min_span_bytes=hint), 2 * total,
                            args.reps),
         # The copy-engine restore's scatter: records in device staging, one wave per KiB of a span.
-        "scatter_pieces_kernel": (lambda: scatter_blocks(stage.data_ptr(), size, dst, *tables,
-                                                         min_span_bytes=hint), 2 * total, args.reps),
+        "scatter_pieces_kernel": (cycling(lambda k: scatter_blocks(stages[k].data_ptr(), size, dst_sets[k], *tables,
+                                                                   min_span_bytes=hint)), 2 * total, args.reps),
         "sha256_kernel": (lambda: _check(lib, lib.kvsnap_sha256_records(
             stage.data_ptr(), size, size, session, sha.data_ptr(), stream.cuda_stream)), total, 1),
         # The gather with every record's CRC32C folded in, into device records on a full grid, and its finish
         # (the save's record bytes and CRC32Cs from one read of the cache): read + write, like the gather.
-        "gather_checked_kernel": (lambda: (_check(lib, lib.kvsnap_gather_blocks_checked(
-            records_at.data_ptr(), ids.data_ptr(), session, *(t.data_ptr() for t in tables), tables[0].numel(), None,
-            0, 0, partial.data_ptr(), stream.cuda_stream)), _check(lib, lib.kvsnap_restore_checked_crc32c(
-                partial.data_ptr(), session, tables[0].data_ptr(), tables[3].data_ptr(), tables[0].numel(), size,
-                crc.data_ptr(), stream.cuda_stream))), 2 * total, args.reps),
+        "gather_checked_kernel": (cycling(gather_checked), 2 * total, args.reps),
         # Its finish alone (every record's CRC32C from its spans' partials): a few microseconds, not HBM-bound.
         "restore_checked_finish_kernel": (lambda: _check(lib, lib.kvsnap_restore_checked_crc32c(
             partial.data_ptr(), session, tables[0].data_ptr(), tables[3].data_ptr(), tables[0].numel(), size,
@@ -1108,33 +1133,36 @@ def run_kernels(args):
     # its loads from the cache and its words written to the records, one launch; read + write, like the gather.
     groups = plane.group_tables()
     if groups is not None:
-        fused = torch.empty(total, dtype=torch.uint8, device="cuda")
+        fused = [torch.empty(total, dtype=torch.uint8, device="cuda") for _ in range(rot)]
         fused_crc = torch.empty(session, dtype=torch.int32, device="cuda")
-        runs["gather_crc_kernel"] = (gather_crc32c_launcher(ids, *groups, size, fused.data_ptr(), size, fused_crc),
-                                     2 * total, args.reps)
+        launches = [gather_crc32c_launcher(id_sets[k], *groups, size, fused[k].data_ptr(), size, fused_crc)
+                    for k in range(rot)]
+        runs["gather_crc_kernel"] = (cycling(lambda k: launches[k]()), 2 * total, args.reps)
     out = {}
     for name, (fn, algorithmic, reps) in runs.items():
-        fn()
-        ms = median_ms(torch, stream, fn, reps=reps, batch=1 if name == "sha256_kernel" else 4)
+        for _ in range(rot):
+            fn()
+        ms = median_ms(torch, stream, fn, reps=reps, batch=1 if name == "sha256_kernel" else 4 * rot)
         out[name] = {"ms": round(ms, 4), "algorithmic_bytes": algorithmic,
                      "gbps": round(algorithmic / ms / 1e6, 1)}
     out["sha256_kernel"]["issue_roofline"] = sha_issue_bound(size, session, out["sha256_kernel"]["ms"],
                                                           sha_round_rate(torch))
-    # The checked gather's CRC32Cs against the CRC kernel's over the same records (the last run of each).
-    runs["crc_records_kernel"][0]()
+    # The checked gather's CRC32Cs against the CRC kernel's over the same records (set 0's).
+    runs["gather_pieces_kernel"][0].on(0)
+    runs["crc_records_kernel"][0].on(0)
     want = crc.clone()
-    runs["gather_checked_kernel"][0]()
+    gather_checked(0)
     torch.cuda.synchronize()
     out["gather_checked_kernel"]["crc32c_equal_crc_kernel"] = bool(torch.equal(want, crc))
     if groups is not None:     # its records against the gather kernel's, its CRC32Cs against the CRC kernel's
-        runs["gather_pieces_kernel"][0]()
-        runs["gather_crc_kernel"][0]()
+        launches[0]()
         torch.cuda.synchronize()
-        out["gather_crc_kernel"]["records_equal_gather"] = bool(torch.equal(fused, stage))
+        out["gather_crc_kernel"]["records_equal_gather"] = bool(torch.equal(fused[0], stage))
         out["gather_crc_kernel"]["crc32c_equal_crc_kernel"] = bool(torch.equal(want, fused_crc))
     staged.close()
     plane.close()
     return {"workload": "kernels", "snapshot_bytes": total, "layout": args.layout, "kv_heads": args.kv_heads,
+            "rotate": rot,
             "span_bytes": sorted({s[3] for s in plane.spans()}), "kernels": out,
             "note": "restore_kernel reads pinned host records (link) and writes HBM; bytes counted both ways"}
 
@@ -1510,6 +1538,8 @@ def main():
     parser.add_argument("--workload", choices=("save-restore", "disk-fork", "rotating-fp8", "turns", "cpu-roundtrip",
                                                "kernels", "duplex", "ttft"), default="save-restore")
     parser.add_argument("--reps", type=int, default=5, help="kernels, ttft: timed repetitions per kernel / arm")
+    parser.add_argument("--rotate", type=int, default=1,
+                        help="kernels: HBM kernels cycle over this many block sets and buffers (no cache reuse)")
     parser.add_argument("--kv-heads", type=int, default=8, choices=(1, 2, 4, 8),
                         help="kernels: KV heads in the cache, 8 / TP for one tensor-parallel rank's shard")
     parser.add_argument("--hash-depth", type=int, default=2,

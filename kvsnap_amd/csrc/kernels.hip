@@ -1031,8 +1031,8 @@ __device__ __forceinline__ void crc_gather_zero(int count, u32x4* v) {
 
 // The landed batch's words to the record (groups g .. g + count - 1 at `record`).  Ordinary stores: the
 // records are read again soon (the device-to-host copy, SHA-256), and a session of up to a few hundred MB
-// stays in the last-level cache between (nontemporal stores measured 4.7 against 5.7 TB/s at a TP = 8
-// shard's 151 MB, and 5.0 against 4.8 at 1.2 GB).
+// stays in the last-level cache between.  Into buffers the cache does not hold, nontemporal stores ran
+// alike (4.5-4.7 TB/s at a TP = 8 shard).
 __device__ __forceinline__ void crc_gather_store(char* __restrict__ record, int g, int count, uint32_t lane,
                                                  const u32x4* v) {
 #pragma unroll
