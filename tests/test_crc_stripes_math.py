@@ -20,7 +20,9 @@ kvsnap_crc32c_extend, csrc/dataplane/io.cpp:39-44); a variant that combines
 the chains in the wrong order must fail.  It also replays the kernel's LDS
 addressing (v_perm_b32 byte moves into a per-lane column constant): every
 lane's lookups of the private slicing and advance tables land in its own
-bank and on the entry the fill put there.
+bank and on the entry the fill put there.  And it replays the addresses the
+aligned kernels' first batch loads (its one path with no branches, clamped):
+every one is a word of the record, and every word folded is the stripe's own.
 """
 import functools
 import operator
@@ -241,3 +243,50 @@ def test_the_private_tables_fill_the_lds_once_and_every_lane_reads_its_own_bank_
                 assert lds[address] == GN[nibble][(x >> (4 * nibble)) & 15]
                 found ^= lds[address]
             assert found == gf_mul(ADVANCE, x)
+
+
+# ---------------------------------------------------------------- the aligned kernels' first-batch addresses
+
+
+def first_batch_loads(start, groups, lane):
+    """crc_stripe_first's loads (kernels.hip, aligned records): per chain, the record offset loaded.  A chain
+    past the stripe's groups loads the batch's last group again, a word of front padding the record's first
+    word (crc_first_words_kept zeroes both once they have landed)."""
+    lead = (-start) // GROUP if start < 0 else 0
+    count = min(CHAINS, groups - lead)
+    at = start + lead * GROUP
+    return lead, count, [max(at + min(c, count - 1) * GROUP + lane * RUN, 0) for c in range(CHAINS)]
+
+
+@pytest.mark.parametrize("record_bytes,n_records", [
+    (16, 1), (16, 300), (48, 7), (1040, 2), (1280, 29), (12000, 8192), (12288, 3), (17408, 5000), (20480, 4096),
+    (294912, 512), (2359296, 512), (4096 * 1024 + 16, 3), (36 * 1024 * 9 + 16, 1000),
+])
+def test_the_aligned_first_batch_loads_only_record_words(record_bytes, n_records):
+    """Every offset the aligned kernels' first batch loads (clamped chains included, for every stripe and
+    lane) lies inside the record, and every word the batch folds (chains below its count, lanes past the
+    padding) is the stripe's own."""
+    groups, stripes, pad = plan(record_bytes, n_records)
+    for j in range(stripes):
+        start = j * groups * GROUP - pad
+        for lane in range(LANES):
+            lead, count, loads = first_batch_loads(start, groups, lane)
+            assert count >= 1
+            for off in loads:
+                assert 0 <= off <= record_bytes - RUN, (record_bytes, j, lane, off)
+            for c in range(count):
+                word = start + (lead + c) * GROUP + lane * RUN
+                if word >= 0:
+                    assert loads[c] == word, (record_bytes, j, c, lane)
+                else:
+                    assert c == 0 and word > -GROUP     # only chain 0 can hold padding, less than a group
+
+
+def test_an_unclamped_first_batch_would_load_outside_the_record():
+    """The replay catches the mistake it guards against: without the clamp to the record's first word, a
+    16-byte record's padding lanes would load before the record."""
+    groups, stripes, pad = plan(16, 1)
+    start = -pad
+    lead = (-start) // GROUP
+    assert min(start + lead * GROUP + lane * RUN for lane in range(LANES)) < 0
+    assert all(first_batch_loads(start, groups, lane)[2][0] == 0 for lane in range(LANES - 1))
