@@ -451,7 +451,7 @@ constexpr int kCrcThreads = 1024;
 constexpr int kCrcWaves = kCrcThreads / 64;
 constexpr int kCrcRun = 16;                  // bytes one lane folds per group: one 16-byte word
 constexpr int kCrcChains = 6;                // groups per batch, each its own chain
-constexpr bool kCrcNontemporal = true;       // streaming loads
+constexpr int kCrcLoadPolicy = 2;           // the buffer loads' cache-policy bits: nt, streaming loads
 constexpr int kCrcRunWords = kCrcRun / 16;
 constexpr int kCrcBatchWords = kCrcChains * kCrcRunWords;  // 16-byte loads per lane per batch
 constexpr int kCrcGroup = 64 * kCrcRun;      // one wave's group
@@ -527,17 +527,45 @@ __device__ __forceinline__ void crc_load_run(const uint8_t* __restrict__ rec, in
     }
 }
 
-// A batch of whole groups of record bytes at record offset `at` (>= 0, 16-byte aligned): chain c's run at
-// v[c * kCrcRunWords ...].
+// Global-address-space views of memory, for record addresses the kernels pass through an empty asm
+// statement (crc_opaque): loads through a kernel argument's pointer count as invariant, and the compiler
+// moved them past the table fill and its barrier, to where they are used.
+using GlobalByte = const __attribute__((address_space(1))) uint8_t;
+using GlobalWord = const __attribute__((address_space(1))) u32x4;
+
+__device__ __forceinline__ GlobalByte* crc_opaque(const void* p) {
+    GlobalByte* g = (GlobalByte*)p;
+    asm volatile("" : "+s"(g));
+    return g;
+}
+
+// A wave-uniform 64-bit value moved to scalar registers (lane 0's copy).
+__device__ __forceinline__ uint64_t uniform64(uint64_t x) {
+    const uint32_t lo = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(x));
+    const uint32_t hi = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(x >> 32));
+    return (static_cast<uint64_t>(hi) << 32) | lo;
+}
+
+// A raw buffer resource over [base, base + bytes): the third word of gfx9's untyped buffer descriptor.
+constexpr int kBufferWord3 = 0x00020000;
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t crc_buffer(const void* base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, static_cast<int>(bytes), kBufferWord3);
+}
+
+// A batch of whole groups of record bytes at record offset `at` (>= 0): chain c's run at v[c].  Buffer
+// loads: the record's address and the batch's offset in scalar registers, each lane's offset (lane * 16,
+// the same every batch) in one vector register.  With a 64-bit address per lane in vector registers the
+// compiler put an `s_waitcnt vmcnt(0)` at the head of the batch loop, before the next batch was issued, so
+// the loads in flight drained every other batch.  The resource ends at the batch's end: a load past it
+// would read zeros, never another allocation.
 __device__ __forceinline__ void crc_load_batch(const uint8_t* __restrict__ rec, int64_t at, uint32_t lane, u32x4* v) {
-    const u32x4* p = reinterpret_cast<const u32x4*>(rec + at + static_cast<int64_t>(lane) * kCrcRun);
+    static_assert(kCrcRunWords == 1, "one word per chain and batch");
+    const __amdgpu_buffer_rsrc_t buffer =
+        crc_buffer(rec + at, static_cast<uint32_t>(kCrcChains * kCrcGroup));
 #pragma unroll
     for (int c = 0; c < kCrcChains; ++c)
-#pragma unroll
-        for (int k = 0; k < kCrcRunWords; ++k) {
-            const u32x4* q = p + c * (kCrcGroup / 16) + k;
-            v[c * kCrcRunWords + k] = kCrcNontemporal ? __builtin_nontemporal_load(q) : *q;
-        }
+        v[c] = __builtin_amdgcn_raw_buffer_load_b128(buffer, lane * kCrcRun, c * kCrcGroup, kCrcLoadPolicy);
 }
 
 // Any batch: the first may hold front padding, the last may hold fewer than kCrcChains groups.
@@ -738,13 +766,7 @@ __device__ __forceinline__ void crc_stripe_first(const uint8_t* __restrict__ rec
         return;
     }
     const int at32 = static_cast<int>(at);  // in (-1024, 2^31)
-    // An opaque copy of the record's address (in the global address space, so the loads stay global loads):
-    // loads through the kernel's read-only argument count as invariant, and the compiler moved them past
-    // the table fill and its barrier, to where they are used.
-    using GlobalByte = const __attribute__((address_space(1))) uint8_t;
-    using GlobalWord = const __attribute__((address_space(1))) u32x4;
-    GlobalByte* base = (GlobalByte*)rec;
-    asm volatile("" : "+s"(base));
+    GlobalByte* base = crc_opaque(rec);  // in scalar registers (crc_opaque)
 #pragma unroll
     for (int c = 0; c < kCrcChains; ++c) {
         const int cc = c < count ? c : count - 1;
@@ -1007,19 +1029,25 @@ __global__ __launch_bounds__(256) void crc_combine_kernel(const uint32_t* __rest
 // the groups' table built once per layout on the host.  A record's front
 // padding (the stripe plan's) is whole groups, which are skipped.
 
-using GlobalWord = const __attribute__((address_space(1))) u32x4;
-
 // The loads of the batch of record groups g, g + 1, ..., g + count - 1 (count >= 1) of `block` into v:
 // chains past `count` load the last of them again (crc_gather_zero then zeroes them).  The group's source
 // address is wave-uniform (scalar loads of the groups' table); lane l loads its 16 bytes.
 __device__ __forceinline__ void crc_gather_load(const int64_t* __restrict__ group_bases,
                                                 const int64_t* __restrict__ group_pitches, int64_t block, int g,
                                                 int count, uint32_t lane, u32x4* v) {
+    // The groups' table is constant while the kernel runs: read through the constant address space, its
+    // entries are scalar loads.  Through a global pointer the compiler loaded one of them with a vector load,
+    // and the wait for it drained the batch in flight.
+    using Table = const __attribute__((address_space(4))) int64_t;
+    Table* bases = (Table*)group_bases;
+    Table* pitches = (Table*)group_pitches;
 #pragma unroll
     for (int c = 0; c < kCrcChains; ++c) {
         const int at = g + (c < count ? c : count - 1);
-        const uint64_t src = static_cast<uint64_t>(group_bases[at] + block * group_pitches[at]);
-        v[c] = __builtin_nontemporal_load(reinterpret_cast<GlobalWord*>(src + lane * kCrcRun));
+        const __amdgpu_buffer_rsrc_t buffer =
+            crc_buffer(reinterpret_cast<const void*>(uniform64(static_cast<uint64_t>(bases[at] + block * pitches[at]))),
+                       kCrcGroup);
+        v[c] = __builtin_amdgcn_raw_buffer_load_b128(buffer, lane * kCrcRun, 0, kCrcLoadPolicy);
     }
 }
 
