@@ -349,8 +349,9 @@ def run_save_restore(args):
     layers, num_blocks, block_size, tokens = 36, 16384, 16, 8192
     session = tokens // block_size
     caches, backing = synth.make_caches(layers, num_blocks, block_size=block_size, layout=args.layout)
-    # Nothing else runs on the GPU here, so the restore kernel reads the pinned records in place (about 3 %
-    # faster than the copy engines, the library's default for serving beside a decode).
+    # Nothing else runs on the GPU here, so the restore kernel reads the pinned records in place (about 1 %
+    # faster than the copy engines, the library's default for serving beside a decode; --restore-mode dma
+    # measures that default).
     plane = TorchBlockDataPlane(caches, block_size, session * layers * 65536 + (64 << 20),
                                 restore_mode=args.restore_mode or "kernel")
     plane.warm_up()
