@@ -1149,3 +1149,19 @@ def test_the_groups_table_follows_the_spans_and_is_refused_for_spans_that_are_no
     assert odd.group_tables() is None
     host_kernels.fused = False
     assert plane_over(caches).group_tables() is None
+
+
+def test_a_restore_stream_without_a_fast_engine_pair_is_reported(caplog):
+    """The copy-engine pick keeps its best candidate either way; when none overlapped the copy stream's engine
+    as the fast engines do, the plane says so in a warning (the pair it kept and every candidate's)."""
+    accepted = {"candidates": 1, "both_ways_gbps": 96.1, "accepted": True, "tried_both_ways_gbps": [96.1]}
+    missed = {"candidates": 4, "both_ways_gbps": 92.5, "accepted": False,
+              "tried_both_ways_gbps": [57.7, 92.5, 57.7, 57.7]}
+    with caplog.at_level("WARNING", logger="kvsnap_amd.dataplane"):
+        assert not dataplane.report_engine_pick(None)
+        assert not dataplane.report_engine_pick(accepted)
+        assert not caplog.records
+        assert dataplane.report_engine_pick(missed)
+    (record,) = caplog.records
+    assert record.levelname == "WARNING"
+    assert "92.5 GB/s" in record.getMessage() and "[57.7, 92.5, 57.7, 57.7]" in record.getMessage()
