@@ -915,6 +915,48 @@ def test_the_gather_with_crc32c_gives_the_oracle_s_records_and_crc32cs(planes, o
     assert np.array_equal(host_copy(backing), before)
 
 
+@pytest.mark.parametrize("groups,n,blocks_total,seed", [
+    (1, 5, 9, 41),          # one-group records: every stripe a single partial batch
+    (7, 300, 320, 42),      # odd group count, many records a workgroup
+    (300, 40, 48, 43),      # long records, several stripes each
+    (17, 5000, 5100, 44),   # more records than one round of the grid
+])
+def test_the_gather_with_crc32c_follows_any_groups_table(oracle_lib, groups, n, blocks_total, seed):
+    """kvsnap_gather_crc32c through the C-ABI over a random groups' table, not a plane's: each 1 KiB group of a
+    record comes from one of two regions of different block pitch, at a random KiB of the block's row, in any
+    order and some twice.  Every record equals the oracle's gather of its block by the same table, every
+    CRC32C the oracle's (csrc/dataplane/io.cpp:39-44), and nothing past a record is written."""
+    rng = random.Random(seed)
+    pitches = (9 * 1024, 3 * 1024 + 1024)                   # bytes per block in each region
+    starts = (0, blocks_total * pitches[0])
+    total = starts[1] + blocks_total * pitches[1]
+    cache = torch.randint(0, 256, (total,), dtype=torch.uint8, device="cuda",
+                          generator=torch.Generator(device="cuda").manual_seed(seed))
+    picks = []
+    for _ in range(groups):
+        region = rng.randrange(2)
+        picks.append((region, rng.randrange(pitches[region] // 1024)))
+    bases = [cache.data_ptr() + starts[r] + 1024 * k for r, k in picks]
+    group_pitches = [pitches[r] for r, _ in picks]
+    blocks = [rng.randrange(blocks_total) for _ in range(n)]
+    host = cache.cpu().numpy()
+    expected = np.stack([np.concatenate([host[starts[r] + b * pitches[r] + 1024 * k:][:1024] for r, k in picks])
+                         for b in blocks])
+    size, gap = groups * 1024, 48
+    pitch = size + gap
+    out = torch.full((n * pitch,), 0x5A, dtype=torch.uint8, device="cuda")
+    crcs = torch.zeros(n, dtype=torch.int32, device="cuda")
+    device_tables = [torch.tensor(v, dtype=torch.int64, device="cuda") for v in (blocks, bases, group_pitches)]
+    print(f"gather with CRC32C, random table: {groups} groups, n={n}, seed={seed}", flush=True)
+    gather_crc32c_launcher(*device_tables, size, out.data_ptr(), pitch, crcs)()
+    torch.cuda.synchronize()
+    written = out.cpu().numpy().reshape(n, pitch)
+    assert np.array_equal(written[:, :size], expected)
+    assert (written[:, size:] == 0x5A).all()
+    assert [value & 0xFFFFFFFF for value in crcs.tolist()] == [oracle_lib.crc32c(r.tobytes()) for r in expected]
+    assert np.array_equal(cache.cpu().numpy(), host)
+
+
 @pytest.mark.parametrize("tokens", [12 * BLOCK_SIZE, 12 * BLOCK_SIZE - 7])
 def test_a_hashed_direct_save_is_one_checked_gather_and_its_digests_are_the_oracle_s(planes, oracle_lib, tokens):
     """save_mode="direct" with digests: the checked gather writes the pinned records and their device copy and
