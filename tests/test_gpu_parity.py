@@ -337,7 +337,7 @@ def test_crc32c_and_sha256_kernels_on_odd_record_sizes(hip_library, oracle_lib, 
 @pytest.mark.parametrize("record_bytes,n", [(12000, 8192), (20380, 2048), (70000, 2048), (40968, 1024),
                                              (294912, 512), (589840, 16)])
 def test_crc32c_kernel_on_the_stripe_plans_of_many_records(hip_library, oracle_lib, record_bytes, n):
-    """Records in the stripe plans the CRC32C launch takes (1 KiB groups, 8 chains per lane): one stripe of
+    """Records in the stripe plans the CRC32C launch takes (1 KiB groups, 6 chains per lane): one stripe of
     12 groups with a partial first group (12000 bytes), two stripes of 10 (20380), two of 35 whose first
     group is all padding (70000), unaligned records (40968), a tensor-parallel shard's records (294912:
     eight stripes of 36 groups) -- all combined inside their workgroup -- and 58 stripes of 10 groups,
@@ -355,6 +355,27 @@ def test_crc32c_kernel_on_the_stripe_plans_of_many_records(hip_library, oracle_l
     got = out.cpu().numpy().astype(np.uint32)
     bad = np.flatnonzero(got != want)
     assert bad.size == 0, (record_bytes, n, bad[:8])
+
+
+@pytest.mark.parametrize("record_bytes,n,pitch", [((1 << 31) - 1024, 1, (1 << 31) - 1024),
+                                                  ((1 << 31) + 48, 2, (1 << 31) + 64)])
+def test_crc32c_kernel_on_records_of_two_gib(hip_library, oracle_lib, record_bytes, n, pitch):
+    """The largest record the aligned kernels take (2 GiB - 1 KiB, 32-bit word offsets) and records past 2 GiB,
+    which the host sends down the unaligned path (64-bit offsets, 64 stripes of 32 MiB and a combine launch):
+    every CRC32C equals the oracle's (csrc/dataplane/io.cpp:39-44)."""
+    lib = kernel_library()
+    data = torch.randint(0, 256, (n * pitch,), dtype=torch.uint8, device="cuda")
+    out = torch.zeros(n, dtype=torch.int32, device="cuda")
+    work_bytes = int(lib.kvsnap_crc32c_workspace_bytes(record_bytes, n))
+    work = torch.empty(max(work_bytes, 16), dtype=torch.uint8, device="cuda")
+    print(f"CRC32C of {n} records of {record_bytes} B, pitch {pitch}", flush=True)
+    _check(lib, lib.kvsnap_crc32c_records(data.data_ptr(), record_bytes, pitch, n, 0, out.data_ptr(),
+                                          work.data_ptr(), work_bytes, torch.cuda.current_stream().cuda_stream))
+    torch.cuda.synchronize()
+    host = data.cpu().numpy()
+    want = [oracle_lib.crc32c_at(host.ctypes.data + r * pitch, record_bytes) for r in range(n)]
+    assert [value & 0xFFFFFFFF for value in out.tolist()] == want
+    del data, host, work
 
 
 @pytest.mark.parametrize("n", [1, 31, 33, 64, 65, 131])
