@@ -546,7 +546,8 @@ __device__ __forceinline__ uint64_t uniform64(uint64_t x) {
     return (static_cast<uint64_t>(hi) << 32) | lo;
 }
 
-// A raw buffer resource over [base, base + bytes): the third word of gfx9's untyped buffer descriptor.
+// A raw buffer resource over [base, base + bytes) (stride 0, so a load past `bytes` reads zeros).
+// kBufferWord3 is the descriptor's last dword on gfx9: data format 32 in bits 15-18, every other field zero.
 constexpr int kBufferWord3 = 0x00020000;
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t crc_buffer(const void* base, uint32_t bytes) {
