@@ -1138,7 +1138,7 @@ def early_report_scenario(planes):
 
 def test_an_early_reported_restore_is_complete_for_the_engine_stream(planes):
     """The early-report protocol's ordering, with no wall-clock bound (the poll's latency is checked by
-    tests/test_zz_timing.py, collected after every parity test)."""
+    tests/test_zy_timing.py, collected after every parity test)."""
     early_report_scenario(planes)
 
 
