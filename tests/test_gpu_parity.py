@@ -1042,20 +1042,23 @@ def test_a_checked_restore_loads_clean_blocks_and_reports_a_corrupt_one_only_aft
     staged.close()
 
 
+@pytest.mark.parametrize("heads", [1, 2, 4])
 @pytest.mark.parametrize("layout", ["kv_split", "vllm"])
 @pytest.mark.parametrize("restore_mode", ["kernel", "dma"])
-def test_a_tensor_parallel_shard_round_trips_with_short_spans(planes, oracle_lib, layout, restore_mode):
-    """One TP = 8 rank's shard of Qwen3-8B (1 KV head: 4 KiB K/V spans, 8 KiB vLLM spans), where the copy
-    launches put several spans in one workgroup: the gathered records equal the oracle's fill, their
-    digests the oracle's, and the restore is the identity, through the restore kernel and the copy engines."""
-    caches, backing = synth.make_caches(36, 600, heads=1, layout=layout)
-    plane = planes(caches, capacity=128 * 36 * 8192 + (64 << 20), restore_mode=restore_mode)
-    assert plane.min_span_bytes == (4096 if layout == "kv_split" else 8192)
+def test_a_tensor_parallel_shard_round_trips_with_short_spans(planes, oracle_lib, layout, restore_mode, heads):
+    """One tensor-parallel rank's shard of Qwen3-8B (TP = 8, 4 and 2: 1, 2 and 4 KV heads, 4-16 KiB K/V spans,
+    8-32 KiB vLLM spans), where the copy launches put several spans in one workgroup and a hashed save takes
+    the gather with CRC32C: the gathered records equal the oracle's fill, their digests the oracle's, and the
+    restore is the identity, through the restore kernel and the copy engines."""
+    caches, backing = synth.make_caches(36, 600, heads=heads, layout=layout)
+    plane = planes(caches, capacity=128 * 36 * 8192 * heads + (64 << 20), restore_mode=restore_mode)
+    assert plane.min_span_bytes == (4096 if layout == "kv_split" else 8192) * heads
+    assert plane.group_tables() is not None
     keep = synth.fill(plane, 3)
     torch.cuda.synchronize()
     del keep
     size = plane.block_bytes
-    assert size == 36 * 8192
+    assert size == 36 * 8192 * heads
     saved, restored = synth.block_tables(600, 128, seed_source=5, seed_target=6)
     assert max(saved + restored) < 600
     staged = plane.pool.reserve(128 * size)
