@@ -1044,7 +1044,8 @@ def run_duplex(args):
 
 def run_kernels(args):
     """Each kernel of the default workload alone, HIP-event timed on its stream, plus a plain
-    device-to-device copy of the same byte count (the reference point for rocprof's traffic counters)."""
+    device-to-device copy of the same byte count (the reference point for rocprof's traffic counters)
+    and a plain read of the records (what the CRC32C kernel could take at this size)."""
     import torch
     from kvsnap_amd import synth
     from kvsnap_amd.dataplane import (_check, copy_host_blocks, digest_device_records, gather_blocks,
@@ -1088,6 +1089,7 @@ def run_kernels(args):
     records_at = [torch.tensor([st.data_ptr() + i * size for i in range(session)], dtype=torch.int64, device="cuda")
                   for st in stages]
     partial = torch.empty(session * tables[0].numel(), dtype=torch.int32, device="cuda")
+    sink = torch.zeros(4096, dtype=torch.int32, device="cuda")
 
     def cycling(launch):
         """launch(k) on set 0, 1, ..., rot - 1, 0, ... in turn, and launch itself for set k."""
@@ -1109,6 +1111,10 @@ def run_kernels(args):
 
     runs = {
         "plain_copy": (cycling(lambda k: others[k].copy_(stages[k])), 2 * total, args.reps),
+        # The same bytes read and nothing else done with them (kvsnap_read_probe, the CRC32C kernels' 1024-lane
+        # workgroups, one a CU): what a read of this size can take, the CRC32C kernel's own ceiling.
+        "plain_read": (cycling(lambda k: _check(lib, lib.kvsnap_read_probe(
+            stages[k].data_ptr(), total, sink.data_ptr(), stream.cuda_stream))), total, args.reps),
         "gather_pieces_kernel": (cycling(lambda k: gather_blocks(id_sets[k], *tables, stages[k].data_ptr(), size,
                                                                  min_span_bytes=hint)), 2 * total, args.reps),
         # 512 records take the one-launch plan (crc_records_kernel: stripes combined in the workgroup).
@@ -1146,6 +1152,7 @@ def run_kernels(args):
         ms = median_ms(torch, stream, fn, reps=reps, batch=1 if name == "sha256_kernel" else 4 * rot)
         out[name] = {"ms": round(ms, 4), "algorithmic_bytes": algorithmic,
                      "gbps": round(algorithmic / ms / 1e6, 1)}
+    out["crc_records_kernel"]["of_plain_read"] = round(out["plain_read"]["ms"] / out["crc_records_kernel"]["ms"], 3)
     out["sha256_kernel"]["issue_roofline"] = sha_issue_bound(size, session, out["sha256_kernel"]["ms"],
                                                           sha_round_rate(torch))
     # The checked gather's CRC32Cs against the CRC kernel's over the same records (set 0's).

@@ -226,6 +226,15 @@ int kvsnap_sha256_ranges(int count, const uint64_t* records, const uint64_t* rec
  * counterpart: the bench's SHA-256 bound is priced from it. */
 int kvsnap_sha_round_probe(uint32_t seed, int reps, uint64_t* out, uintptr_t stream);
 
+/* The chip's read rate for a buffer of a given size, measured: one launch of
+ * 256 workgroups of 1024 lanes (the CRC32C kernels' shape, one a CU) reads
+ * the `bytes` (a positive multiple of 16, src 16-byte aligned) at `src` with
+ * nontemporal 16-byte loads and does nothing else with them.  sink (4096
+ * device words) receives one word a wave; their XOR is the XOR of the
+ * buffer's 32-bit words.  No reference counterpart: the bench prices the
+ * CRC32C kernels against it at the same size. */
+int kvsnap_read_probe(const void* src, uint64_t bytes, uint32_t* sink, uintptr_t stream);
+
 /* Streams of the data plane's own (no reference counterpart; the reference
  * copies on one stream).  kvsnap_stream_create makes a non-blocking stream of
  * default priority on `device`; kvsnap_stream_destroy waits for its work and

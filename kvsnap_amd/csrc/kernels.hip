@@ -1957,6 +1957,34 @@ __global__ __launch_bounds__(64) void sha_round_probe_kernel(uint32_t seed, int 
     }
 }
 
+// The chip's read rate at a given size, measured: the CRC32C kernels' shape
+// (one 1024-lane workgroup a CU) reading `words` 16-byte words with
+// nontemporal loads, four in flight per lane, and nothing else.  Each wave
+// XORs what it read into one word of sink (16 a workgroup), so the XOR of
+// sink is the XOR of the buffer's 32-bit words.
+constexpr int kReadProbeLanes = 1024, kReadProbeUnroll = 4, kReadProbeGroups = 256;
+
+__global__ __launch_bounds__(kReadProbeLanes) void read_probe_kernel(const u32x4* __restrict__ src, uint64_t words,
+                                                                      uint32_t* __restrict__ sink) {
+    const uint64_t stride = static_cast<uint64_t>(gridDim.x) * kReadProbeLanes * kReadProbeUnroll;
+    uint64_t i = static_cast<uint64_t>(blockIdx.x) * kReadProbeLanes * kReadProbeUnroll + threadIdx.x;
+    u32x4 acc = {0, 0, 0, 0};
+    for (; i + (kReadProbeUnroll - 1) * kReadProbeLanes < words; i += stride) {
+        u32x4 v[kReadProbeUnroll];
+#pragma unroll
+        for (int u = 0; u < kReadProbeUnroll; ++u) v[u] = __builtin_nontemporal_load(src + i + u * kReadProbeLanes);
+#pragma unroll
+        for (int u = 0; u < kReadProbeUnroll; ++u) acc ^= v[u];
+    }
+#pragma unroll
+    for (int u = 0; u < kReadProbeUnroll; ++u)
+        if (i + u * kReadProbeLanes < words) acc ^= src[i + u * kReadProbeLanes];
+    uint32_t x = acc.x ^ acc.y ^ acc.z ^ acc.w;
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) x ^= __shfl_xor(x, o);
+    if ((threadIdx.x & 63) == 0) sink[blockIdx.x * (kReadProbeLanes / 64) + threadIdx.x / 64] = x;
+}
+
 // ----------------------------------------------------------------- host helpers
 
 uint32_t host_gf_mul(uint32_t a, uint32_t b) {
@@ -2680,6 +2708,17 @@ int kvsnap_sha_round_probe(uint32_t seed, int reps, uint64_t* out, uintptr_t str
         hipLaunchKernelGGL(sha_round_probe_kernel, dim3(1), dim3(64), 0, reinterpret_cast<hipStream_t>(stream), seed,
                            reps, out);
         check_launch("SHA-256 round probe");
+    });
+}
+
+int kvsnap_read_probe(const void* src, uint64_t bytes, uint32_t* sink, uintptr_t stream) {
+    return guard([&] {
+        if (!src || reinterpret_cast<uintptr_t>(src) % 16 || bytes == 0 || bytes % 16)
+            throw std::runtime_error("read probe: a 16-byte aligned buffer of a positive multiple of 16 bytes");
+        if (!sink || reinterpret_cast<uintptr_t>(sink) % 4) throw std::runtime_error("read probe: bad sink");
+        hipLaunchKernelGGL(read_probe_kernel, dim3(kReadProbeGroups), dim3(kReadProbeLanes), 0,
+                           reinterpret_cast<hipStream_t>(stream), static_cast<const u32x4*>(src), bytes / 16, sink);
+        check_launch("read probe");
     });
 }
 

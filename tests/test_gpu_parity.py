@@ -1313,3 +1313,18 @@ def test_the_sha_round_probe_times_the_round_sequence(hip_library):
     assert 36 <= slot < 60, slot
     assert 0.8 < ghz < 2.6, ghz
     assert sums[0] != sums[1]
+
+
+@pytest.mark.parametrize("nbytes", [16, 4096 + 16, (1 << 20) + 48, 512 * 294912 + 16])
+def test_the_read_probe_reads_every_word_once(hip_library, nbytes):
+    """kvsnap_read_probe: the XOR of its sink is the XOR of the buffer's 32-bit words, for a buffer smaller
+    than one wave's loads, a ragged one, and a TP = 8 shard's records with one word more (its tail path)."""
+    generator = torch.Generator(device="cuda").manual_seed(nbytes)
+    buffer = torch.randint(-2**31, 2**31, (nbytes // 4,), dtype=torch.int32, device="cuda", generator=generator)
+    sink = torch.zeros(4096, dtype=torch.int32, device="cuda")
+    lib = kernel_library()
+    _check(lib, lib.kvsnap_read_probe(buffer.data_ptr(), nbytes, sink.data_ptr(),
+                                      torch.cuda.current_stream().cuda_stream))
+    torch.cuda.synchronize()
+    want = np.bitwise_xor.reduce(buffer.cpu().numpy().view(np.uint32))
+    assert np.bitwise_xor.reduce(sink.cpu().numpy().view(np.uint32)) == want
