@@ -1044,8 +1044,9 @@ def run_duplex(args):
 
 def run_kernels(args):
     """Each kernel of the default workload alone, HIP-event timed on its stream, plus a plain
-    device-to-device copy of the same byte count (the reference point for rocprof's traffic counters)
-    and a plain read of the records (what the CRC32C kernel could take at this size)."""
+    device-to-device copy of the same byte count (the reference point for rocprof's traffic counters),
+    a plain read of the records (what the CRC32C kernel could take at this size) and a contiguous copy of
+    them with the gather and scatter kernels' shape (what those could take)."""
     import torch
     from kvsnap_amd import synth
     from kvsnap_amd.dataplane import (_check, copy_host_blocks, digest_device_records, gather_blocks,
@@ -1115,6 +1116,10 @@ def run_kernels(args):
         # workgroups, one a CU): what a read of this size can take, the CRC32C kernel's own ceiling.
         "plain_read": (cycling(lambda k: _check(lib, lib.kvsnap_read_probe(
             stages[k].data_ptr(), total, sink.data_ptr(), stream.cuda_stream))), total, args.reps),
+        # The records copied contiguously with the gather and scatter kernels' shape (kvsnap_copy_probe: one
+        # 64-lane workgroup a KiB, nothing scattered): their own ceiling at this size.
+        "streaming_copy": (cycling(lambda k: _check(lib, lib.kvsnap_copy_probe(
+            stages[k].data_ptr(), others[k].data_ptr(), total, stream.cuda_stream))), 2 * total, args.reps),
         "gather_pieces_kernel": (cycling(lambda k: gather_blocks(id_sets[k], *tables, stages[k].data_ptr(), size,
                                                                  min_span_bytes=hint)), 2 * total, args.reps),
         # 512 records take the one-launch plan (crc_records_kernel: stripes combined in the workgroup).
@@ -1153,6 +1158,8 @@ def run_kernels(args):
         out[name] = {"ms": round(ms, 4), "algorithmic_bytes": algorithmic,
                      "gbps": round(algorithmic / ms / 1e6, 1)}
     out["crc_records_kernel"]["of_plain_read"] = round(out["plain_read"]["ms"] / out["crc_records_kernel"]["ms"], 3)
+    for name in ("gather_pieces_kernel", "scatter_pieces_kernel"):
+        out[name]["of_streaming_copy"] = round(out["streaming_copy"]["ms"] / out[name]["ms"], 3)
     out["sha256_kernel"]["issue_roofline"] = sha_issue_bound(size, session, out["sha256_kernel"]["ms"],
                                                           sha_round_rate(torch))
     # The checked gather's CRC32Cs against the CRC kernel's over the same records (set 0's).

@@ -235,6 +235,14 @@ int kvsnap_sha_round_probe(uint32_t seed, int reps, uint64_t* out, uintptr_t str
  * CRC32C kernels against it at the same size. */
 int kvsnap_read_probe(const void* src, uint64_t bytes, uint32_t* sink, uintptr_t stream);
 
+/* The chip's rate for a contiguous device-to-device copy of a given size,
+ * measured: `bytes` (a positive multiple of 16, at most 1 TiB; src and dst
+ * 16-byte aligned, not overlapping) copied with the gather and scatter
+ * kernels' shape, one 64-lane workgroup a KiB and one nontemporal 16-byte
+ * load and store a lane.  No reference counterpart: the bench prices the
+ * gather and scatter kernels against it at the same size. */
+int kvsnap_copy_probe(const void* src, void* dst, uint64_t bytes, uintptr_t stream);
+
 /* Streams of the data plane's own (no reference counterpart; the reference
  * copies on one stream).  kvsnap_stream_create makes a non-blocking stream of
  * default priority on `device`; kvsnap_stream_destroy waits for its work and

@@ -1985,6 +1985,15 @@ __global__ __launch_bounds__(kReadProbeLanes) void read_probe_kernel(const u32x4
     if ((threadIdx.x & 63) == 0) sink[blockIdx.x * (kReadProbeLanes / 64) + threadIdx.x / 64] = x;
 }
 
+// The chip's rate for a contiguous copy of a given size, measured: the pieces
+// kernels' shape (one 64-lane workgroup a KiB, one nontemporal 16-byte load
+// and store a lane) with no tables, no spans and no scattered side.
+__global__ __launch_bounds__(64) void copy_probe_kernel(const u32x4* __restrict__ src, u32x4* __restrict__ dst,
+                                                        uint64_t words) {
+    const uint64_t i = static_cast<uint64_t>(blockIdx.x) * 64 + threadIdx.x;
+    if (i < words) __builtin_nontemporal_store(__builtin_nontemporal_load(src + i), dst + i);
+}
+
 // ----------------------------------------------------------------- host helpers
 
 uint32_t host_gf_mul(uint32_t a, uint32_t b) {
@@ -2719,6 +2728,19 @@ int kvsnap_read_probe(const void* src, uint64_t bytes, uint32_t* sink, uintptr_t
         hipLaunchKernelGGL(read_probe_kernel, dim3(kReadProbeGroups), dim3(kReadProbeLanes), 0,
                            reinterpret_cast<hipStream_t>(stream), static_cast<const u32x4*>(src), bytes / 16, sink);
         check_launch("read probe");
+    });
+}
+
+int kvsnap_copy_probe(const void* src, void* dst, uint64_t bytes, uintptr_t stream) {
+    return guard([&] {
+        if (!src || !dst || (reinterpret_cast<uintptr_t>(src) | reinterpret_cast<uintptr_t>(dst)) % 16 || bytes == 0 ||
+            bytes % 16 || bytes > (uint64_t{1} << 40))
+            throw std::runtime_error("copy probe: 16-byte aligned buffers of a positive multiple of 16 bytes, at most 1 TiB");
+        const uint64_t words = bytes / 16;
+        hipLaunchKernelGGL(copy_probe_kernel, dim3(static_cast<uint32_t>((words + 63) / 64)), dim3(64), 0,
+                           reinterpret_cast<hipStream_t>(stream), static_cast<const u32x4*>(src),
+                           static_cast<u32x4*>(dst), words);
+        check_launch("copy probe");
     });
 }
 

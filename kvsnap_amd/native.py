@@ -65,6 +65,7 @@ KERNEL_SIGNATURES = {
     "kvsnap_sha256_ranges": "int <- int ptr ptr ptr ptr ptr ptr ptr ptr stream",
     "kvsnap_sha_round_probe": "int <- u32 int ptr stream",
     "kvsnap_read_probe": "int <- ptr u64 ptr stream",
+    "kvsnap_copy_probe": "int <- ptr ptr u64 stream",
     "kvsnap_stream_create": "int <- int size*",
     "kvsnap_stream_destroy": "int <- stream",
     "kvsnap_hold_stream": "int <- stream int",

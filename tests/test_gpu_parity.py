@@ -1328,3 +1328,16 @@ def test_the_read_probe_reads_every_word_once(hip_library, nbytes):
     torch.cuda.synchronize()
     want = np.bitwise_xor.reduce(buffer.cpu().numpy().view(np.uint32))
     assert np.bitwise_xor.reduce(sink.cpu().numpy().view(np.uint32)) == want
+
+
+@pytest.mark.parametrize("nbytes", [16, 4096 + 16, (1 << 20) + 48, 512 * 294912 + 16])
+def test_the_copy_probe_copies_every_word_and_nothing_past(hip_library, nbytes):
+    """kvsnap_copy_probe: the destination equals the source, and the 64 bytes after it are untouched."""
+    generator = torch.Generator(device="cuda").manual_seed(nbytes + 1)
+    src = torch.randint(0, 256, (nbytes,), dtype=torch.uint8, device="cuda", generator=generator)
+    dst = torch.full((nbytes + 64,), 0xA5, dtype=torch.uint8, device="cuda")
+    lib = kernel_library()
+    _check(lib, lib.kvsnap_copy_probe(src.data_ptr(), dst.data_ptr(), nbytes, torch.cuda.current_stream().cuda_stream))
+    torch.cuda.synchronize()
+    assert torch.equal(dst[:nbytes], src)
+    assert bool((dst[nbytes:] == 0xA5).all())

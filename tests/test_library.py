@@ -92,3 +92,14 @@ def test_the_read_probe_refuses_a_bad_buffer_before_any_gpu_call():
     for src, nbytes, sink in ((0, 16, 16), (8, 16, 16), (16, 0, 16), (16, 24, 16), (16, 16, 0), (16, 16, 2)):
         assert hip.kvsnap_read_probe(src, nbytes, sink, 0) == -1
         assert b"read probe" in hip.kvsnap_cuda_error()
+
+
+def test_the_copy_probe_refuses_a_bad_buffer_before_any_gpu_call():
+    """kvsnap_copy_probe checks its arguments on the host first (no GPU here)."""
+    hip = C.CDLL(str(HIP_LIBRARY))
+    hip.kvsnap_copy_probe.argtypes = [C.c_void_p, C.c_void_p, C.c_uint64, C.c_size_t]
+    hip.kvsnap_cuda_error.restype = C.c_char_p
+    for src, dst, nbytes in ((0, 16, 16), (16, 0, 16), (8, 16, 16), (16, 24, 16), (16, 16, 0), (16, 32, 40),
+                             (16, 32, (1 << 40) + 16)):
+        assert hip.kvsnap_copy_probe(src, dst, nbytes, 0) == -1
+        assert b"copy probe" in hip.kvsnap_cuda_error()
