@@ -503,9 +503,19 @@ def run_save_restore(args):
     sha_out = torch.empty((session, 32), dtype=torch.uint8, device="cuda")
     sha_alone_ms = median_ms(torch, stream, lambda: _check(lib, lib.kvsnap_sha256_records(
         records.data_ptr(), size, size, session, sha_out.data_ptr(), stream.cuda_stream)), reps=3)
-    del records, work, sha_out
+    # What the same bytes take with nothing but the copy or the read: a contiguous copy with the gather and
+    # scatter kernels' shape (kvsnap_copy_probe) and a plain read with the CRC32C kernel's (kvsnap_read_probe).
+    copied = torch.empty(total, dtype=torch.uint8, device="cuda")
+    sink = torch.zeros(4096, dtype=torch.int32, device="cuda")
+    copy_probe_ms = median_ms(torch, stream, lambda: _check(lib, lib.kvsnap_copy_probe(
+        records.data_ptr(), copied.data_ptr(), total, stream.cuda_stream)), reps=5, batch=4)
+    read_probe_ms = median_ms(torch, stream, lambda: _check(lib, lib.kvsnap_read_probe(
+        records.data_ptr(), total, sink.data_ptr(), stream.cuda_stream)), reps=5, batch=4)
+    del records, work, sha_out, copied
     scatter_achieved = 2 * total / (scatter_ms * 1e6)
     crc_achieved = total / (crc_alone_ms * 1e6)
+    copy_probe = 2 * total / (copy_probe_ms * 1e6)
+    read_probe = total / (read_probe_ms * 1e6)
     cpu = None if args.no_cpu_baseline else cpu_baseline(layers, 65536, session, args.cpu_seconds)
     out = {
         "metric": "8k Qwen3-8B KV restore/save GB/s and ms; % of host-link and HBM roofline",
@@ -562,15 +572,22 @@ def run_save_restore(args):
                      "peak": HBM_PEAK_GBPS, "unit": "GB/s", "frac": round(gather_achieved / HBM_PEAK_GBPS, 4),
                      "launches_per_save": gather_per_save,
                      "traffic": measured_traffic("gather_pieces_kernel"), "algorithmic_bytes": 2 * total,
-                     "traffic_source": "profiles/qwen3-8b-8k-kernels.traffic.md (rocprofv3 FETCH_SIZE, WRITE_SIZE)"},
+                     "traffic_source": "profiles/qwen3-8b-8k-kernels.traffic.md (rocprofv3 FETCH_SIZE, WRITE_SIZE)",
+                     "copy_probe_gbps": round(copy_probe, 1),
+                     "frac_of_copy_probe": round(gather_achieved / copy_probe, 4),
+                     "copy_probe": "kvsnap_copy_probe: the same bytes copied contiguously, a 64-lane workgroup a KiB"},
         "link_roofline": {"kernel": "restore_kernel", "bound": "host-link", "achieved": round(restore_link, 2),
                           "peak": round(h2d_peak, 2), "unit": "GB/s", "frac": round(restore_link / h2d_peak, 4)},
         "scatter_roofline": {"kernel": "scatter_pieces_kernel (device records to cache)", "bound": "hbm",
                              "achieved": round(scatter_achieved, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
-                             "frac": round(scatter_achieved / HBM_PEAK_GBPS, 4), "ms": round(scatter_ms, 4)},
+                             "frac": round(scatter_achieved / HBM_PEAK_GBPS, 4), "ms": round(scatter_ms, 4),
+                             "frac_of_copy_probe": round(scatter_achieved / copy_probe, 4)},
         "crc_roofline": {"kernel": "crc_records_kernel", "bound": "hbm", "achieved": round(crc_achieved, 1),
                          "peak": HBM_PEAK_GBPS, "unit": "GB/s", "frac": round(crc_achieved / HBM_PEAK_GBPS, 4),
-                         "ms": round(crc_alone_ms, 4), "in_step_ms": round(crc["avg_ms"], 4)},
+                         "ms": round(crc_alone_ms, 4), "in_step_ms": round(crc["avg_ms"], 4),
+                         "read_probe_gbps": round(read_probe, 1),
+                         "frac_of_read_probe": round(crc_achieved / read_probe, 4),
+                         "read_probe": "kvsnap_read_probe: the same bytes read with this kernel's workgroup shape"},
         "sha256": {"kernel": "sha256_kernel", "ms": round(sha_alone_ms, 3),
                    "gbps": round(total / (sha_alone_ms * 1e6), 2), "records": session,
                    "in_step_ms": round(sha["avg_ms"], 3),
