@@ -29,6 +29,8 @@ import re
 import struct
 import uuid
 
+import numpy as np
+
 from .native_io import NativeIO, get_io_backend
 
 HEADER = struct.Struct("<8sIQI8s")
@@ -208,7 +210,42 @@ class BlobDirectory:
 
     def _read_plan(self, segments, address, block_bytes, first_block):
         """(blob path, pinned target, payload offset, length, CRC32C, block index) per segment, after checking
-        that the segments map blocks ``first_block, first_block + 1, ...`` one whole KV block each."""
+        that the segments map blocks ``first_block, first_block + 1, ...`` one whole KV block each.
+
+        The checks run a column at a time (a plan of 2048 blocks took 2.6 ms
+        segment by segment, in the restore's time before its first copy); a
+        plan that fails one is walked segment by segment for its first error.
+        """
+        n = len(segments)
+        try:
+            ids = [segment["blob_id"] for segment in segments]
+            firsts = [segment["first_block"] for segment in segments]
+            counts = [segment["nblocks"] for segment in segments]
+            offsets = [segment["offset"] for segment in segments]
+            lengths = [segment["length"] for segment in segments]
+            crcs = [segment["crc32c"] for segment in segments]
+        except (KeyError, TypeError):
+            return self._read_plan_by_segment(segments, address, block_bytes, first_block)
+        if not (n and firsts == list(range(first_block, first_block + n)) and counts.count(1) == n
+                and set(map(type, offsets)) == {int} and min(offsets) >= 0
+                and set(map(type, lengths)) == {int} and lengths.count(block_bytes) == n
+                and set(map(type, ids)) == {str}):
+            return self._read_plan_by_segment(segments, address, block_bytes, first_block)
+        # n ids of 64 lowercase hex digits each: the joined ids are ASCII, n - 1 newlines at every 65th byte
+        # and nothing else but hex digits.
+        try:
+            joined = "\n".join(ids).encode("ascii")
+        except UnicodeEncodeError:
+            joined = b""
+        if (len(joined) != 65 * n - 1 or joined.count(b"\n") != n - 1 or joined[64::65] != b"\n" * (n - 1)
+                or joined.translate(None, b"0123456789abcdef\n")):
+            return self._read_plan_by_segment(segments, address, block_bytes, first_block)
+        prefix = self._blob_dir_str + "/"
+        return list(zip([prefix + blob_id + ".blob" for blob_id in ids],
+                        [address + i * block_bytes for i in range(n)], [HEADER.size + offset for offset in offsets],
+                        lengths, crcs, range(first_block, first_block + n)))
+
+    def _read_plan_by_segment(self, segments, address, block_bytes, first_block):
         plan = []
         for position, segment in enumerate(segments):
             block = first_block + position
@@ -314,12 +351,18 @@ class BlobRingReader:
         self.lib, self.plan = io.lib, plan
         n = len(plan)
         self.chunks = -(-n // per_chunk)
-        names = [os.fsencode(job[0]) for job in plan]
-        self._paths = (C.c_char_p * n)(*names)
-        self._offsets = (C.c_uint64 * n)(*[job[2] - HEADER.size for job in plan])
-        self._crcs = (C.c_uint32 * n)(*[job[4] for job in plan])
+        # The paths as one buffer of NUL-terminated names and a table of pointers into it (one encode and a
+        # vector pass, where a bytes object and a ctypes pointer per path took about 1 ms for 2048 blocks).
+        self._names = os.fsencode("\0".join(job[0] for job in plan)) + b"\0"
+        ends = np.flatnonzero(np.frombuffer(self._names, dtype=np.uint8) == 0)
+        if len(ends) != n:
+            raise CorruptSnapshotError("a blob path holds a NUL byte")
+        base = C.cast(C.c_char_p(self._names), C.c_void_p).value
+        self._paths = np.concatenate(([0], ends[:-1] + 1)).astype(np.uint64) + np.uint64(base)
+        self._offsets = np.array([job[2] - HEADER.size for job in plan], dtype=np.uint64)
+        self._crcs = np.array([job[4] & 0xFFFFFFFF for job in plan], dtype=np.uint32)
         self.handle = self.lib.kvsnap_blob_reader_start(
-            C.cast(self._paths, C.c_void_p), C.cast(self._offsets, C.c_void_p), C.cast(self._crcs, C.c_void_p), n,
+            self._paths.ctypes.data, self._offsets.ctypes.data, self._crcs.ctypes.data, n,
             block_bytes, ring, per_chunk, slots, workers, 1 if verify else 0)
         if not self.handle:
             raise RuntimeError("the blob ring reader could not be started")

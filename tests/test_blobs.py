@@ -179,3 +179,38 @@ def test_the_ring_reader_leaves_crc_checks_to_the_caller_when_asked(tmp_path):
     with pytest.raises(RuntimeError, match="native"):
         with BlobDirectory(tmp_path, io_backend="python").ring_reader(segments, C.addressof(ring), 4096, 3, 1):
             pass
+
+
+def test_the_read_plan_checks_a_whole_plan_as_the_walk_over_its_segments_does(tmp_path):
+    """The read plan's column checks pass exactly the plans that the segment-by-segment walk passes, and a
+    plan that fails one gets the walk's error (a newline inside an id, upper-case or non-ASCII hex, a gap, a
+    segment of two blocks, a negative offset, a bool offset, a float length, a missing key)."""
+    store = BlobDirectory(tmp_path, io_backend="native")
+    ids = [hashlib.sha256(bytes([i])).hexdigest() for i in range(5)]
+    segments = [dict(blob_id=blob_id, first_block=3 + i, nblocks=1, offset=64 * i, length=4096, crc32c=i)
+                for i, blob_id in enumerate(ids)]
+    walked = store._read_plan_by_segment(segments, 1 << 20, 4096, 3)
+    walk, store._read_plan_by_segment = store._read_plan_by_segment, None      # a valid plan is not walked
+    plan = store._read_plan(segments, 1 << 20, 4096, 3)
+    store._read_plan_by_segment = walk
+    assert plan == walked
+    assert plan[4] == (str(store.path(ids[4])), (1 << 20) + 4 * 4096, HEADER.size + 256, 4096, 4, 7)
+    assert store._read_plan([], 0, 4096, 0) == []
+    bad = [(1, dict(blob_id=ids[1][:30] + "\n" + ids[1][31:]), "identifier"),
+           (2, dict(blob_id=ids[2].upper()), "identifier"),
+           (4, dict(blob_id=ids[4][:63] + "é"), "identifier"),
+           (3, dict(blob_id=ids[3][:63]), "identifier"),
+           (0, dict(first_block=9), "noncontiguous"),
+           (3, dict(nblocks=2), "noncontiguous"),
+           (1, dict(offset=-1), "block size"),
+           (2, dict(offset=True), "block size"),
+           (2, dict(length=4096.0), "block size")]
+    for position, change, match in bad:
+        changed = list(segments)
+        changed[position] = dict(segments[position], **change)
+        with pytest.raises(CorruptSnapshotError, match=match):
+            store._read_plan(changed, 1 << 20, 4096, 3)
+    changed = list(segments)
+    changed[1] = {key: value for key, value in segments[1].items() if key != "crc32c"}
+    with pytest.raises(KeyError):
+        store._read_plan(changed, 1 << 20, 4096, 3)
