@@ -353,12 +353,12 @@ class BlobRingReader:
         self.chunks = -(-n // per_chunk)
         # The paths as one buffer of NUL-terminated names and a table of pointers into it (one encode and a
         # vector pass, where a bytes object and a ctypes pointer per path took about 1 ms for 2048 blocks).
-        self._names = os.fsencode("\0".join(job[0] for job in plan)) + b"\0"
+        self._names = os.fsencode("\0".join(job[0] for job in plan)) + b"\0" if n else b""
         ends = np.flatnonzero(np.frombuffer(self._names, dtype=np.uint8) == 0)
         if len(ends) != n:
             raise CorruptSnapshotError("a blob path holds a NUL byte")
         base = C.cast(C.c_char_p(self._names), C.c_void_p).value
-        self._paths = np.concatenate(([0], ends[:-1] + 1)).astype(np.uint64) + np.uint64(base)
+        self._paths = np.concatenate(([0], ends[:-1] + 1)).astype(np.uint64)[:n] + np.uint64(base or 0)
         self._offsets = np.array([job[2] - HEADER.size for job in plan], dtype=np.uint64)
         self._crcs = np.array([job[4] & 0xFFFFFFFF for job in plan], dtype=np.uint32)
         self.handle = self.lib.kvsnap_blob_reader_start(
