@@ -171,8 +171,8 @@ def link_peaks(torch, staged, stream, nbytes):
 
 
 def host_threads():
-    """(os.cpu_count(), CPUs this process may run on, threads the baseline uses).  A one-GPU box gives a
-    process a share of 16 CPUs whatever the machine has, so the widest leg runs on at most 16 threads."""
+    """(os.cpu_count(), CPUs this process may run on, threads the baseline uses).  One GPU's share of a
+    host is taken as 16 CPUs whatever the machine has, so the widest leg runs on at most 16 threads."""
     count = os.cpu_count() or 1
     allowed = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else count
     return count, allowed, max(1, min(16, allowed))
@@ -301,7 +301,7 @@ def cpu_baseline(layers, span, records=512, seconds_per_leg=0.6):
             "sample": (f"the {records}-record snapshot ({records} x {record} B = {total} B) gathered from and "
                        f"scattered into a {host_blocks}-block host cache; best of repeated runs per leg; pread from "
                        f"a page-cached file"),
-            "threads_note": "widest leg = min(16, CPUs this process may use): a one-GPU box's CPU share"}
+            "threads_note": "widest leg = min(16, CPUs this process may use): one GPU's share of the host's CPUs"}
 
 
 def measured_traffic(kernel):

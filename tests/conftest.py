@@ -32,7 +32,7 @@ def pytest_collection_modifyitems(config, items):
 
 @pytest.fixture(scope="session")
 def hip_library():
-    """The built HIP library; on a GPU box its absence is a failure, not a skip."""
+    """The built HIP library; on a machine with a GPU its absence is a failure, not a skip."""
     from kvsnap_amd.dataplane import kernel_library, resolve_cuda_library
     path = resolve_cuda_library()
     assert path.is_file(), f"HIP library not built at {path}"
