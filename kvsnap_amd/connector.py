@@ -11,7 +11,7 @@ the reference's names and arguments (``vllm.py:436-699``): registration,
 ``get_block_ids_with_load_errors`` and ``shutdown``.
 
 The scheduler role (snapshot store, manifests, leases, prefix matching) is
-control plane and is not part of this build: constructing the connector for
+control plane and is not implemented here: constructing the connector for
 it raises, and its hooks raise ``NotImplementedError``.  The scheduler hands
 the worker :class:`KvsnapConnectorMetadata` (the step's load and save
 :class:`~kvsnap_amd.worker.Transfer` lists) and reads back
@@ -65,7 +65,7 @@ class KvsnapConnector(KVConnectorBase_V1):
 
     def __init__(self, vllm_config, role, kv_cache_config=None):
         if role != KVConnectorRole.WORKER:
-            raise NotImplementedError("this build provides the connector's worker role only: the scheduler side "
+            raise NotImplementedError("kvsnap_amd provides the connector's worker role only: the scheduler side "
                                       "(snapshot store, manifests, leases) is not part of it")
         parallel = vllm_config.parallel_config
         if getattr(parallel, "pipeline_parallel_size", 1) != 1 or getattr(parallel, "data_parallel_size", 1) != 1:
@@ -139,10 +139,10 @@ class KvsnapConnector(KVConnectorBase_V1):
         if self.worker.dataplane is not None:
             self.worker.dataplane.close()
 
-    # ---- scheduler hooks: not part of this build --------------------------------
+    # ---- scheduler hooks: not implemented here ---------------------------------
 
     def _scheduler_only(self, *args, **kwargs):
-        raise NotImplementedError("the connector's scheduler side is not part of this build")
+        raise NotImplementedError("the connector's scheduler side is not implemented in kvsnap_amd")
 
     get_num_new_matched_tokens = _scheduler_only
     update_state_after_alloc = _scheduler_only

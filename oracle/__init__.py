@@ -1,7 +1,7 @@
 """CPU oracle for the KV snapshot dataplane -- TEST INFRASTRUCTURE ONLY.
 
 Only ``tests/``, ``__graft_entry__.smoke()`` and ``bench.py``'s ``cpu_baseline``
-leg may import this package, and only as the checker.  ``kvsnap_amd`` never
+leg may import this package, and only to check results.  ``kvsnap_amd`` never
 imports, links or calls anything here: its paths run on the HIP library and
 fail loudly without it.
 
@@ -206,8 +206,8 @@ def zero_tail(record: np.ndarray, layers, valid: int):
     offsets, geometry, offset = [], [], 0
     for layer in layers:
         if len(layer["shape"]) == 4:
-            # [2, N, H, C] K/V-split layer (this build's extension of the
-            # reference layout): the same rule applied to its K and V halves.
+            # [2, N, H, C] K/V-split layer (an extension of the reference
+            # layout): the same rule applied to its K and V halves.
             _, n, h, c = layer["shape"]
             _, sn, sh, _ = layer["stride"]
             half = layer["bytes"] // 2

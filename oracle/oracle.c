@@ -2,7 +2,7 @@
  * CPU oracle for the KV snapshot dataplane -- TEST INFRASTRUCTURE ONLY.
  *
  * A plain-C restatement of the reference's byte path, used by tests/, by
- * __graft_entry__.smoke() and by bench.py's cpu_baseline leg as the checker.
+ * __graft_entry__.smoke() and by bench.py's cpu_baseline leg, to check results.
  * Nothing in kvsnap_amd/ may link, load or call it.
  *
  * Each function names the reference file:line it restates (paths relative to
