@@ -1,7 +1,8 @@
 # Builds the reference's own C++ sources for this path, straight from the
-# read-only reference tree, into oracle/_ref/ (git-ignored and listed in
-# .gpurunignore: only the CPU test suite uses them, and no reference code goes
-# to the GPU box).  Nothing here is copied into the repository.
+# read-only reference tree, into oracle/_ref/ (git-ignored and kept out of the
+# snapshots that GPU runs receive: only the CPU test suite uses them, and no
+# reference code runs beside the GPU).  Nothing here is copied into the
+# repository.
 #
 #   make -f oracle/ref.mk            (REF defaults to /root/reference)
 #
